@@ -1,0 +1,194 @@
+/* tensafe_he.h — C ABI of the MI355X (gfx950) CKKS engine for the encrypted
+ * LoRA-delta path.
+ *
+ * This is the drop-in boundary under the reference's Python-facing backend
+ * interface (the PyO3 module `tensafe_he`,
+ * tensafe-he/crates/tensafe-he-python/src/lib.rs:18-405). Every entry point
+ * below names the reference function it replaces. Results are bit-identical
+ * to the reference CPU backend (tensafe-he-core) for the same inputs and the
+ * same seeded randomness.
+ *
+ * Conventions
+ *  - All functions return 0 on success and a negative TH_E* code on error;
+ *    th_last_error() returns a thread-local message for the last failure.
+ *    No C++ exception or panic crosses this boundary.
+ *  - Handles (th_ctx, th_sk, th_pk, th_ct, th_pt) are opaque and owned by the
+ *    library; release them with the matching *_free. Ciphertext, key and
+ *    plaintext data stay resident in device memory (HBM) for their lifetime.
+ *  - Host input arrays are caller-owned and only read during the call; host
+ *    output arrays are caller-owned and fully written before return.
+ *  - `has_seed == 0` draws the seed from the OS (the reference's
+ *    TenSafeRng::from_entropy); otherwise a fresh ChaCha20 stream seeded with
+ *    `seed` is used for that call (lib.rs:93-96, rng.rs:38-68).
+ *  - One HIP stream per context: a context is thread-compatible, not
+ *    thread-safe. Operations are asynchronous on that stream except those
+ *    that return host data, which synchronise it once per call.
+ *  - Ciphertext layout: c0 then c1, each `limbs` limb-polynomials of N
+ *    little-endian u64 residues in [0, q_l), NTT (evaluation) domain.
+ */
+#ifndef TENSAFE_HE_H
+#define TENSAFE_HE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct th_ctx th_ctx;
+typedef struct th_sk th_sk;
+typedef struct th_pk th_pk;
+typedef struct th_ct th_ct;
+typedef struct th_pt th_pt;
+
+enum {
+  TH_OK = 0,
+  TH_EINVAL = -1,   /* bad argument (reference: PyValueError / assert!) */
+  TH_EDEVICE = -2,  /* no usable gfx950 device or a HIP runtime error */
+  TH_ENOMEM = -3,   /* device or host allocation failed */
+  TH_ESTATE = -4    /* operation not valid for this object (e.g. rescale at 1 limb) */
+};
+
+/* Message of the last failing call on this thread (never NULL). */
+const char* th_last_error(void);
+/* Library version string. */
+const char* th_version(void);
+/* Number of visible HIP devices. */
+int th_device_count(int* count);
+
+/* ---------------------------------------------------------------- context */
+/* Replaces CkksContext::new (lib.rs:35-56, ciphertext.rs:61-74).
+ * moduli == NULL selects the reference chain for N in {8192, 16384, 32768}
+ * (params.rs:66-126); otherwise `L` distinct NTT-friendly primes
+ * (q = 1 mod 2N, q < 2^62) define the chain. scale_bits must be 40
+ * (params.rs:9). */
+int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale_bits, int device,
+                  th_ctx** out);
+int th_ctx_free(th_ctx* ctx);
+/* Replaces the num_slots / poly_mod_degree getters (lib.rs:79-88) and
+ * get_backend_info's num_limbs (lib.rs:282-294). moduli_out may be NULL. */
+int th_ctx_info(const th_ctx* ctx, uint32_t* N, uint32_t* L, uint64_t* moduli_out);
+/* Wait for all work queued on the context's stream. */
+int th_ctx_sync(th_ctx* ctx);
+/* The context's HIP stream (hipStream_t), for callers that order their own work after it. */
+int th_ctx_stream(th_ctx* ctx, void** stream);
+
+/* ---------------------------------------------------------------- keys */
+/* Replaces CkksContext.keygen (lib.rs:91-99, ciphertext.rs:77-103). */
+int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out);
+/* Replaces CkksContext.keygen_public (lib.rs:102-110, ciphertext.rs:114-154). */
+int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, th_pk** out);
+int th_sk_free(th_sk* sk);
+int th_pk_free(th_pk* pk);
+/* Secret key s (NTT domain, L x N) to host; for tests and key escrow. */
+int th_sk_download(th_ctx* ctx, const th_sk* sk, uint64_t* out);
+/* Public key (b, a), each L x N, to host. */
+int th_pk_download(th_ctx* ctx, const th_pk* pk, uint64_t* b, uint64_t* a);
+
+/* ---------------------------------------------------------------- encryption */
+/* Replaces CkksContext.encrypt (lib.rs:115-138, ciphertext.rs:167-229).
+ * z has n <= N/2 values (zero-padded; longer input is truncated as lib.rs:124-126 does). */
+int th_encrypt(th_ctx* ctx, const th_sk* sk, const double* z, size_t n, uint64_t seed, int has_seed,
+               th_ct** out);
+/* Replaces CkksContext.batch_encrypt (lib.rs:230-258): secret-key encryption
+ * of `count` inputs (input i is z + i*stride with lens[i] values) drawing
+ * from ONE ChaCha20 stream in order, as the reference's shared RNG does. */
+int th_encrypt_batch(th_ctx* ctx, const th_sk* sk, const double* z, const uint64_t* lens, size_t stride,
+                     size_t count, uint64_t seed, int has_seed, th_ct** outs);
+/* Replaces CkksContext.encrypt_pk (lib.rs:141-164, ciphertext.rs:240-319). */
+int th_encrypt_pk(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, uint64_t seed, int has_seed,
+                  th_ct** out);
+/* encrypt_pk with caller-supplied randomness, for parity runs: u holds the
+ * values sample_ternary(rng, N, 3) returns ({0,1,2} meaning -1, 0, +1;
+ * sampling.rs:17-29, ciphertext.rs:256-268), e0 and e1 the rounded Gaussian
+ * samples (sampling.rs:51-58), N entries each. */
+int th_encrypt_pk_explicit(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, const uint8_t* u,
+                           const int64_t* e0, const int64_t* e1, th_ct** out);
+/* `count` encrypt_pk calls in one batch: input i is z + i*stride (n values),
+ * seeded with seeds[i]. Replaces a loop of encrypt_pk (the engine's one
+ * encrypt per layer input, inference_engine.py:1272). */
+int th_encrypt_pk_batch(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, size_t stride, size_t count,
+                        const uint64_t* seeds, th_ct** outs);
+
+/* ---------------------------------------------------------------- plaintexts and products */
+/* Replaces CkksContext::encode_to_ntt (ciphertext.rs:539-545): the cached
+ * LoRA-A plaintext batches (inference_engine.py:1037-1074). */
+int th_encode_to_ntt(th_ctx* ctx, const double* z, size_t n, th_pt** out);
+int th_pt_free(th_pt* pt);
+int th_pt_download(th_ctx* ctx, const th_pt* pt, uint64_t* out);
+/* Replaces CkksContext.ct_pt_mul / TenSafeCiphertext.__mul__
+ * (lib.rs:178-195, :336-356; ciphertext.rs:408-418). */
+int th_ct_pt_mul(th_ctx* ctx, const th_ct* ct, const double* pt, size_t n, th_ct** out);
+/* Replaces CkksContext::ct_pt_mul_ntt (ciphertext.rs:422-429). */
+int th_ct_pt_mul_ntt(th_ctx* ctx, const th_ct* ct, const th_pt* pt, th_ct** out);
+/* `count` ct_pt_mul_ntt products in one launch: outs[i] = cts[i] x pts[i]
+ * (the ZeRo-MOAI column-packed matvec batches, inference_engine.py:1292-1316). */
+int th_ct_pt_mul_ntt_batch(th_ctx* ctx, const th_ct* const* cts, const th_pt* const* pts, size_t count,
+                           th_ct** outs);
+/* Replace CkksContext.ct_add / ct_sub (lib.rs:198-215, ciphertext.rs:435-466). */
+int th_ct_add(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out);
+int th_ct_sub(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out);
+/* Replaces CkksContext.rescale (lib.rs:218-225, ciphertext.rs:476-535). */
+int th_rescale(th_ctx* ctx, const th_ct* ct, th_ct** out);
+/* `count` rescales in one batch (all inputs must have the same limb count). */
+int th_rescale_batch(th_ctx* ctx, const th_ct* const* cts, size_t count, th_ct** outs);
+
+/* ---------------------------------------------------------------- decryption */
+/* Replaces CkksContext.decrypt (lib.rs:167-175, ciphertext.rs:327-400):
+ * out receives N/2 doubles. */
+int th_decrypt(th_ctx* ctx, const th_ct* ct, const th_sk* sk, double* out);
+/* Replaces CkksContext.batch_decrypt (lib.rs:261-273) with a GPU-resident
+ * batch: all decrypts and decodes run on the device and the results come
+ * back in one device-to-host copy. out receives count x N/2 doubles. */
+int th_batch_decrypt(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, double* out);
+/* As th_batch_decrypt, but returns only the ZeRo-MOAI segment sums
+ * out[i*cols + c] = sum(dec_i[c*d : (c+1)*d]) (inference_engine.py:1379-1386):
+ * one host sync and count x cols doubles per batch. */
+int th_batch_decrypt_segsum(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, uint32_t d,
+                            uint32_t cols, double* out);
+/* As th_batch_decrypt, writing count x N/2 doubles to device memory at
+ * dev_out (e.g. a ROCm torch tensor; the engine's decrypt_to_gpu,
+ * inference_engine.py:190-205). The context stream is synchronised before return. */
+int th_batch_decrypt_device(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk,
+                            double* dev_out);
+
+/* ---------------------------------------------------------------- ciphertext objects */
+int th_ct_free(th_ct* ct);
+/* Replace TenSafeCiphertext.num_limbs / scale getters (lib.rs:385-394). */
+int th_ct_info(const th_ct* ct, uint32_t* limbs, double* scale);
+/* c0 and c1 (limbs x N each) to host. */
+int th_ct_download(th_ctx* ctx, const th_ct* ct, uint64_t* c0, uint64_t* c1);
+/* A ciphertext from host residues (limbs x N each, NTT domain). */
+int th_ct_upload(th_ctx* ctx, const uint64_t* c0, const uint64_t* c1, uint32_t limbs, double scale,
+                 th_ct** out);
+/* Wire format of serialize.rs:71-93: [scale f64 LE | c0 | c1]. With buf ==
+ * NULL only *len is set. */
+int th_ct_export(th_ctx* ctx, const th_ct* ct, uint8_t* buf, size_t cap, size_t* len);
+int th_ct_import(th_ctx* ctx, const uint8_t* buf, size_t len, uint32_t limbs, th_ct** out);
+/* Wire format of serialize.rs:48-67: [b | a]. */
+int th_pk_export(th_ctx* ctx, const th_pk* pk, uint8_t* buf, size_t cap, size_t* len);
+int th_pk_import(th_ctx* ctx, const uint8_t* buf, size_t len, th_pk** out);
+
+/* ---------------------------------------------------------------- raw transforms */
+/* In-place forward / inverse negacyclic NTT (ntt.rs:79-141) of `count`
+ * polynomials, each `limbs` consecutive limb-polynomials of N u64 using
+ * moduli q_0 .. q_{limbs-1}. `polys` is a host pointer (on_device == 0) or a
+ * device pointer (on_device == 1; asynchronous on the context stream). */
+int th_ntt_forward_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device);
+int th_ntt_inverse_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device);
+/* Device-memory helpers for callers without their own allocator. */
+int th_dev_alloc(th_ctx* ctx, size_t bytes, void** out);
+int th_dev_free(th_ctx* ctx, void* p);
+int th_memcpy_h2d(th_ctx* ctx, void* dst, const void* src, size_t bytes);
+int th_memcpy_d2h(th_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Times `reps` back-to-back launches of the batched transform of
+ * th_ntt_*_batch(on_device = 1) with HIP events on the context stream;
+ * *avg_ms receives the mean duration of one launch. */
+int th_ntt_time(th_ctx* ctx, uint64_t* dev_polys, size_t count, uint32_t limbs, int inverse, int reps,
+                float* avg_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TENSAFE_HE_H */

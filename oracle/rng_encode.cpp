@@ -1,6 +1,11 @@
 // Oracle: ChaCha20 RNG, samplers and the f64 canonical-embedding encoder.
 // Restates tensafe-he-core/src/rng.rs, sampling.rs and encoding.rs. Test
 // infrastructure only (see oracle.h). Built with -ffp-contract=off.
+#ifndef _GNU_SOURCE
+#define _GNU_SOURCE
+#endif
+#include <math.h>
+
 #include <cmath>
 #include <cstdio>
 #include <stdexcept>
@@ -176,6 +181,14 @@ EncryptPkRandomness sample_encrypt_pk_randomness(TenSafeRng& rng, size_t n) {
   return r;
 }
 
+// cos and sin of one angle. The reference computes `angle.cos()` and
+// `angle.sin()` back to back (encoding.rs:47-48, :72-73); LLVM lowers such a
+// pair of libm calls on one operand to glibc `sincos` on GNU targets, whose
+// results differ from separate cos/sin calls in the last bit for ~0.1% of
+// angles. Calling sincos explicitly keeps that choice independent of the C++
+// compiler's own fusion heuristics. (No reference test pins these values.)
+static inline void sincos_pair(double angle, double* c, double* s) { ::sincos(angle, s, c); }
+
 // encoding.rs:39-80
 FftTables FftTables::make(size_t n) {
   FftTables t;
@@ -185,8 +198,7 @@ FftTables FftTables::make(size_t n) {
   t.twist_im.assign(n, 0.0);
   for (size_t j = 0; j < n; ++j) {
     double angle = PI * (double)j / (double)n;
-    t.twist_re[j] = std::cos(angle);
-    t.twist_im[j] = std::sin(angle);
+    sincos_pair(angle, &t.twist_re[j], &t.twist_im[j]);
   }
   t.bit_rev.assign(n, 0);
   for (size_t i = 0; i < n; ++i) {
@@ -204,8 +216,10 @@ FftTables FftTables::make(size_t n) {
     tim.reserve(half_len);
     for (size_t k = 0; k < half_len; ++k) {
       double angle = -2.0 * PI * (double)k / (double)(2 * half_len);
-      tre.push_back(std::cos(angle));
-      tim.push_back(std::sin(angle));
+      double c, si;
+      sincos_pair(angle, &c, &si);
+      tre.push_back(c);
+      tim.push_back(si);
     }
     t.twiddle_re.push_back(std::move(tre));
     t.twiddle_im.push_back(std::move(tim));

@@ -1,0 +1,228 @@
+// GPU-resident decode of decrypted polynomials (tensafe-he-core/src/encoding.rs
+// :219-239 and :282-315, ciphertext.rs:351-399).
+//
+// Evaluation order and rounding follow the reference exactly (this file is
+// compiled with -ffp-contract=off, twiddles are the host's glibc values), so
+// the decoded slots are bit-identical to the reference CPU decode:
+//   coefficient: centre against q0/2 (or the 2-limb CRT value against
+//                q0*q1/2), convert to f64 (round to nearest even), / scale
+//   twist:       b = c * (cos(pi j/N), -sin(pi j/N))
+//   FFT:         bit-reversal permutation, radix-2 DIT stages with
+//                v = w*x[i1]; x[i0] = u + v; x[i1] = u - v
+//   output:      real parts of the first N/2 values.
+//
+// The N complex values (256 KiB at N = 16384) exceed LDS, so the transform is
+// split: after the bit-reversal, stages 0 .. logN-p-1 act inside 2^p
+// independent parts of N/2^p values (one workgroup each, in LDS); the last p
+// stages combine the parts element-wise in a second kernel, which also forms
+// the ZeRo-MOAI segment sums.
+#include "poly_kernels.h"
+
+namespace th {
+
+__device__ __forceinline__ uint32_t brv_bits(uint32_t x, uint32_t bits) {
+  return bits ? (__brev(x) >> (32 - bits)) : 0;
+}
+
+// Rust `u128 as f64`: round to nearest, ties to even.
+__device__ __forceinline__ double u128_to_f64(uint64_t hi, uint64_t lo) {
+  if (hi == 0) return (double)lo;
+  const int lz = __clzll(hi);
+  const uint64_t h = lz ? ((hi << lz) | (lo >> (64 - lz))) : hi;
+  const uint64_t l = lo << lz;
+  uint64_t mant = h >> 11;
+  const uint64_t rem = h & 0x7FFu;
+  if (rem > 0x400u || (rem == 0x400u && (l != 0 || (mant & 1)))) ++mant;
+  return ldexp((double)mant, 75 - lz);
+}
+
+// Decrypted coefficient j as the reference's f64 value before the twist.
+__device__ __forceinline__ double coeff_value(const DecodeJob& jb, const DecodeConst& dc, uint32_t j,
+                                              uint32_t n) {
+  if (!jb.crt) {
+    const uint64_t c = jb.m[j];
+    const double s = c > dc.half_q0 ? -((double)(dc.q0 - c)) : (double)c;
+    return s / jb.scale;
+  }
+  // ciphertext.rs:360-392
+  const uint64_t m0 = jb.m[j], m1 = jb.m[n + j];
+  const uint64_t m0q1 = m0 < dc.q1 ? m0 : mulmod_barrett(m0, 1, dc.b1);
+  const uint64_t diff = m1 >= m0q1 ? m1 - m0q1 : dc.q1 - m0q1 + m1;
+  const uint64_t k = csub(shoup_lazy(diff, dc.q0_inv_q1, dc.q0_inv_q1_s, dc.q1), dc.q1);
+  // M = m0 + k * q0 (128-bit)
+  uint64_t lo = k * dc.q0;
+  uint64_t hi = __umul64hi(k, dc.q0);
+  lo += m0;
+  hi += lo < m0 ? 1 : 0;
+  if (hi > dc.Q_hi || (hi == dc.Q_hi && lo >= dc.Q_lo)) {  // M >= Q (unreachable for canonical inputs)
+    const uint64_t nlo = lo - dc.Q_lo;
+    hi = hi - dc.Q_hi - (lo < dc.Q_lo ? 1 : 0);
+    lo = nlo;
+  }
+  double v;
+  if (hi > dc.halfQ_hi || (hi == dc.halfQ_hi && lo > dc.halfQ_lo)) {
+    const uint64_t dlo = dc.Q_lo - lo;
+    const uint64_t dhi = dc.Q_hi - hi - (dc.Q_lo < lo ? 1 : 0);
+    v = -u128_to_f64(dhi, dlo);
+  } else {
+    v = u128_to_f64(hi, lo);
+  }
+  return v / jb.scale;
+}
+
+constexpr int DEC_THREADS = 1024;
+
+template <int LP>
+__global__ __launch_bounds__(DEC_THREADS) void k_decode_parts(const DecodeJob* __restrict__ jobs, const DecodeConst* dcp,
+                                                              const double* __restrict__ twist_re,
+                                                              const double* __restrict__ twist_im,
+                                                              const double* __restrict__ stage_re,
+                                                              const double* __restrict__ stage_im, uint32_t logn) {
+  extern __shared__ double sh[];
+  const DecodeConst dc = *dcp;
+  const uint32_t n = 1u << logn;
+  const uint32_t M = n >> LP;
+  const uint32_t part = blockIdx.x;
+  const DecodeJob jb = jobs[blockIdx.y];
+  double* re = sh;
+  double* im = sh + M;
+  const uint32_t r = brv_bits(part, LP);
+  const uint32_t lb = logn - LP;
+  for (uint32_t jj = threadIdx.x; jj < M; jj += blockDim.x) {
+    const uint32_t j = (jj << LP) | r;
+    const double c = coeff_value(jb, dc, j, n);
+    const uint32_t pos = brv_bits(jj, lb);
+    re[pos] = c * twist_re[j];
+    im[pos] = -c * twist_im[j];
+  }
+  __syncthreads();
+  for (uint32_t s = 0; s < lb; ++s) {
+    const uint32_t half = 1u << s;
+    const double* wr = stage_re + (half - 1);
+    const double* wi = stage_im + (half - 1);
+    for (uint32_t b = threadIdx.x; b < M / 2; b += blockDim.x) {
+      const uint32_t k = b & (half - 1);
+      const uint32_t i0 = ((b >> s) << (s + 1)) | k;
+      const uint32_t i1 = i0 + half;
+      const double w_re = wr[k], w_im = wi[k];
+      const double x_re = re[i1], x_im = im[i1];
+      const double v_re = w_re * x_re - w_im * x_im;
+      const double v_im = w_re * x_im + w_im * x_re;
+      const double u_re = re[i0], u_im = im[i0];
+      re[i0] = u_re + v_re;
+      im[i0] = u_im + v_im;
+      re[i1] = u_re - v_re;
+      im[i1] = u_im - v_im;
+    }
+    __syncthreads();
+  }
+  double* out = jb.parts + (size_t)part * 2 * M;
+  for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
+    out[i] = re[i];
+    out[M + i] = im[i];
+  }
+}
+
+// complex multiply-accumulate in the reference's order: returns (u + w*x, u - w*x)
+struct Cx {
+  double re, im;
+};
+__device__ __forceinline__ void dit(Cx u, Cx x, double w_re, double w_im, Cx& top, Cx& bot) {
+  const double v_re = w_re * x.re - w_im * x.im;
+  const double v_im = w_re * x.im + w_im * x.re;
+  top.re = u.re + v_re;
+  top.im = u.im + v_im;
+  bot.re = u.re - v_re;
+  bot.im = u.im - v_im;
+}
+
+template <int LP>
+__global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* __restrict__ jobs,
+                                                              const double* __restrict__ stage_re,
+                                                              const double* __restrict__ stage_im, uint32_t logn,
+                                                              uint32_t d, uint32_t cols) {
+  extern __shared__ double dec[];
+  const uint32_t n = 1u << logn;
+  const uint32_t S = n / 2;
+  const uint32_t M = n >> LP;
+  const DecodeJob jb = jobs[blockIdx.x];
+  const double* P = jb.parts;
+  auto at = [&](uint32_t part, uint32_t i) { return Cx{P[(size_t)part * 2 * M + i], P[(size_t)part * 2 * M + M + i]}; };
+  if constexpr (LP == 0) {
+    for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) dec[k] = P[k];
+  } else if constexpr (LP == 1) {
+    const double* wr = stage_re + (S - 1);
+    const double* wi = stage_im + (S - 1);
+    for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) {
+      const Cx u = at(0, k), x = at(1, k);
+      const double v_re = wr[k] * x.re - wi[k] * x.im;
+      dec[k] = u.re + v_re;
+    }
+  } else {  // LP == 2
+    const uint32_t Q4 = n / 4;
+    const double* w1r = stage_re + (Q4 - 1);
+    const double* w1i = stage_im + (Q4 - 1);
+    const double* w2r = stage_re + (S - 1);
+    const double* w2i = stage_im + (S - 1);
+    for (uint32_t k = threadIdx.x; k < Q4; k += blockDim.x) {
+      Cx y0, y1, y2, y3;
+      dit(at(0, k), at(1, k), w1r[k], w1i[k], y0, y1);  // positions k, k + N/4
+      dit(at(2, k), at(3, k), w1r[k], w1i[k], y2, y3);  // positions N/2 + k, 3N/4 + k
+      dec[k] = y0.re + (w2r[k] * y2.re - w2i[k] * y2.im);
+      dec[k + Q4] = y1.re + (w2r[k + Q4] * y3.re - w2i[k + Q4] * y3.im);
+    }
+  }
+  __syncthreads();
+  if (jb.out)
+    for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) jb.out[k] = dec[k];
+  if (jb.seg) {
+    // one wavefront per segment; lane-strided partial sums, then a fixed butterfly tree
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
+    for (uint32_t sg = wave; sg < cols; sg += nwaves) {
+      double acc = 0.0;
+      const uint32_t base = sg * d;
+      for (uint32_t i = lane; i < d; i += 64)
+        if (base + i < S) acc += dec[base + i];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+      if (lane == 0) jb.seg[sg] = acc;
+    }
+  }
+}
+
+size_t decode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
+
+static uint32_t parts_log(uint32_t logn) { return logn <= 13 ? 0 : logn - 13; }
+
+hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* twist_re,
+                         const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
+                         uint32_t d, uint32_t cols, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  const uint32_t lp = parts_log(logn);
+  const uint32_t M = (1u << logn) >> lp;
+  const size_t lds_a = (size_t)2 * M * sizeof(double);
+  const size_t lds_b = (size_t)(1u << logn) / 2 * sizeof(double);
+  hipError_t e;
+#define TH_DEC(LP)                                                                                         \
+  case LP:                                                                                                 \
+    e = hipFuncSetAttribute((const void*)k_decode_parts<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                            (int)lds_a);                                                                   \
+    if (e != hipSuccess) return e;                                                                         \
+    e = hipFuncSetAttribute((const void*)k_decode_final<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                            (int)lds_b);                                                                   \
+    if (e != hipSuccess) return e;                                                                         \
+    hipLaunchKernelGGL(k_decode_parts<LP>, dim3(1u << LP, njobs), dim3(DEC_THREADS), lds_a, s, jobs, dc,   \
+                       twist_re, twist_im, stage_re, stage_im, logn);                                      \
+    hipLaunchKernelGGL(k_decode_final<LP>, dim3(njobs), dim3(DEC_THREADS), lds_b, s, jobs, stage_re,       \
+                       stage_im, logn, d, cols);                                                           \
+    return hipGetLastError();
+  switch (lp) {
+    TH_DEC(0)
+    TH_DEC(1)
+    TH_DEC(2)
+    default: return hipErrorInvalidValue;
+  }
+#undef TH_DEC
+}
+
+}  // namespace th

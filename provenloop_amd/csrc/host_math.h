@@ -1,0 +1,65 @@
+// Host-side arithmetic of the engine: parameter tables, the seeded ChaCha20
+// stream and samplers, and the f64 canonical-embedding encoder.
+//
+// These follow the reference's definitions exactly (they decide ciphertext
+// bits), but are this library's own implementation: the stream is produced in
+// whole 64-byte blocks into a buffer and the encoder runs on flat arrays.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+namespace th {
+
+typedef unsigned __int128 u128;
+
+// Default RNS chains (tensafe-he-core/src/params.rs:66-126).
+bool default_chain(uint32_t n, std::vector<uint64_t>& q);
+bool is_prime(uint64_t n);
+uint64_t powmod(uint64_t b, uint64_t e, uint64_t q);
+uint64_t invmod(uint64_t a, uint64_t q);  // q prime, a != 0
+// First g = 2, 3, ... whose g^((q-1)/2N) is a primitive 2N-th root (rns.rs:124-155).
+uint64_t primitive_2n_root(uint32_t n, uint64_t q);
+
+// Deterministic ChaCha20 stream with the reference's seed expansion and
+// draw helpers (tensafe-he-core/src/rng.rs:31-157).
+class ChaChaStream {
+ public:
+  explicit ChaChaStream(uint64_t seed);
+  static ChaChaStream from_os_entropy();
+  uint32_t u32();
+  uint64_t u64();
+  uint32_t below_u32(uint32_t max);  // rejection sampling, rng.rs:109-120
+  uint64_t below_u64(uint64_t max);  // rng.rs:124-133
+  double unit_open();                // ((u64 >> 11) + 0.5) / 2^53
+  double normal(double sigma);       // Box-Muller cosine branch
+
+ private:
+  void next_block();
+  uint32_t key_[8];
+  uint32_t counter_;
+  uint32_t buf_[16];
+  int pos_;
+};
+
+constexpr double ERROR_SIGMA = 3.19;  // sampling.rs:10
+
+// Ternary draws as sample_ternary(rng, n, 3) stores them: r -> {2, 0, 1}[r].
+void draw_ternary(ChaChaStream& s, size_t n, uint8_t* out);
+// round(gaussian) as i64, half away from zero, saturating (sampling.rs:51-58).
+void draw_gaussian(ChaChaStream& s, size_t n, int64_t* out);
+
+// f64 encoder tables and transforms (tensafe-he-core/src/encoding.rs:24-278).
+struct Encoder {
+  uint32_t n = 0, logn = 0;
+  std::vector<double> twist_re, twist_im;   // cos/sin(pi j / N)
+  std::vector<double> stage_re, stage_im;   // per-stage DIT twiddles, stage s at offset 2^s - 1
+  std::vector<uint32_t> brv;
+  void init(uint32_t n);
+  void fft(double* re, double* im) const;
+  // z (len <= N/2) -> round(coeff * 2^40) as i64 per coefficient.
+  void encode_i64(const double* z, size_t len, int64_t* out) const;
+};
+
+}  // namespace th

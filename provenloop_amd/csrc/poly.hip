@@ -1,0 +1,198 @@
+// Element-wise RNS kernels: fused across limbs, ciphertext components and
+// batch entries. Every launch covers a list of jobs; each job is a run of
+// limb-polynomials with a common layout, and blockIdx.y selects the job.
+// These kernels are HBM-bound (two or three u64 streams per output word).
+#include "poly_kernels.h"
+
+namespace th {
+
+__device__ __forceinline__ uint64_t addmod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
+__device__ __forceinline__ uint64_t submod(uint64_t a, uint64_t b, uint64_t q) {
+  return a >= b ? a - b : a + q - b;
+}
+// tensafe-he-core/src/ciphertext.rs:132-136: e >= 0 ? e % q : q - (|e| % q).
+// |e| < 2^63 < q^2 for every prime used, so the Barrett remainder is exact.
+__device__ __forceinline__ uint64_t signed_residue(int64_t e, const BarrettConst& m) {
+  const uint64_t a = e >= 0 ? (uint64_t)e : (uint64_t)0 - (uint64_t)e;
+  const uint64_t r = a < m.q ? a : mulmod_barrett(a, 1, m);
+  return e >= 0 ? r : m.q - r;
+}
+
+// out[c][l][i] = ct[c][l][i] * pt[l][i] for c in {0,1}, l < limbs
+// (ciphertext.rs:422-429 / rns.rs:243-253), all jobs in one launch.
+__global__ void k_ct_pt_mul(const CtPtJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
+                            uint32_t n) {
+  const CtPtJob jb = jobs[blockIdx.y];
+  const uint32_t per_comp = jb.limbs * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < 2 * per_comp; e += gridDim.x * blockDim.x) {
+    const uint32_t w = e < per_comp ? e : e - per_comp;
+    const uint32_t l = w / n;
+    const uint64_t c = (e < per_comp ? jb.ct0 : jb.ct1)[w];
+    jb.out[e] = mulmod_barrett(c, jb.pt[w], bc[l]);
+  }
+}
+
+// out = a +/- b over 2 * limbs limb-polynomials (ciphertext.rs:435-466).
+__global__ void k_ct_addsub(const AddJob* __restrict__ jobs, const uint64_t* __restrict__ q, uint32_t n) {
+  const AddJob jb = jobs[blockIdx.y];
+  const uint32_t total = 2 * jb.limbs * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const uint32_t l = (e / n) % jb.limbs;
+    const uint64_t m = q[l];
+    jb.out[e] = jb.sub ? submod(jb.a[e], jb.b[e], m) : addmod(jb.a[e], jb.b[e], m);
+  }
+}
+
+// encrypt_pk inputs before the forward NTT (ciphertext.rs:250-296):
+//   M_l = (m + e0) mod q_l, U_l = u mod q_l, E1_l = e1 mod q_l.
+// Layout of dst per job: [M (L) | E1 (L) | U (L)] limb-polynomials.
+__global__ void k_encrypt_prep(const EncPrepJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
+                               uint32_t n, uint32_t L) {
+  const EncPrepJob jb = jobs[blockIdx.y];
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const int64_t m = jb.m[i], e0 = jb.e0[i];
+    const int64_t e1 = jb.e1 ? jb.e1[i] : 0;
+    const uint8_t u = jb.u ? jb.u[i] : 1;
+    for (uint32_t l = 0; l < L; ++l) {
+      const BarrettConst c = bc[l];
+      const uint64_t ql = c.q;
+      jb.dst[(uint64_t)l * n + i] = addmod(signed_residue(m, c), signed_residue(e0, c), ql);
+      if (jb.e1) jb.dst[(uint64_t)(L + l) * n + i] = signed_residue(e1, c);
+      // ciphertext.rs:261-266: 0 -> q-1, 1 -> 0, 2 -> 1
+      if (jb.u) jb.dst[(uint64_t)(2 * L + l) * n + i] = u == 0 ? ql - 1 : (u == 1 ? 0 : 1);
+    }
+  }
+}
+
+// dst[l][i] = x[i] mod q_l for signed integer coefficients (encoding.rs:193-204).
+__global__ void k_signed_to_rns(const int64_t* __restrict__ x, uint64_t* __restrict__ dst,
+                                const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const int64_t v = x[i];
+    for (uint32_t l = 0; l < L; ++l) dst[(uint64_t)l * n + i] = signed_residue(v, bc[l]);
+  }
+}
+
+// out = x - a*s over L x N (keygen_public b = -a*s + e, ciphertext.rs:141-151;
+// secret-key encrypt c0 = -a*s + (m + e), ciphertext.rs:209-222).
+__global__ void k_sub_product(const uint64_t* __restrict__ x, const uint64_t* __restrict__ a,
+                              const uint64_t* __restrict__ s, uint64_t* __restrict__ out,
+                              const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L) {
+  const uint32_t total = L * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const BarrettConst m = bc[e / n];
+    out[e] = submod(x[e], mulmod_barrett(a[e], s[e], m), m.q);
+  }
+}
+
+// c0 = b*U + M, c1 = a*U + E1 in the NTT domain (ciphertext.rs:298-312).
+__global__ void k_encrypt_combine(const EncCombineJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
+                                  uint32_t n, uint32_t L) {
+  const EncCombineJob jb = jobs[blockIdx.y];
+  const uint32_t total = L * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const uint32_t l = e / n;
+    const BarrettConst m = bc[l];
+    const uint64_t U = jb.prep[2 * total + e];
+    const uint64_t bu = mulmod_barrett(jb.pk_b[e], U, m);
+    const uint64_t au = mulmod_barrett(jb.pk_a[e], U, m);
+    jb.out[e] = addmod(bu, jb.prep[e], m.q);
+    jb.out[total + e] = addmod(au, jb.prep[total + e], m.q);
+  }
+}
+
+// Rescale in the coefficient domain (ciphertext.rs:476-535): for every
+// component c and limb l < L-1,
+//   out[c][l] = ((x[c][l] - (x[c][L-1] mod q_l)) mod q_l) * (q_{L-1} mod q_l)^{-1}
+// where x is the inverse-transformed input ciphertext (2 x L limb-polys).
+__global__ void k_rescale_combine(const RescaleJob* __restrict__ jobs, const RescaleConst* __restrict__ rc,
+                                  uint32_t n, uint32_t L) {
+  const RescaleJob jb = jobs[blockIdx.y];
+  const uint32_t Lo = L - 1;
+  const uint32_t total = 2 * Lo * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const uint32_t comp = e / (Lo * n);
+    const uint32_t w = e - comp * Lo * n;
+    const uint32_t l = w / n, i = w - l * n;
+    const RescaleConst c = rc[l];
+    const uint64_t x = jb.coef[((uint64_t)comp * L + l) * n + i];
+    const uint64_t last = jb.coef[((uint64_t)comp * L + Lo) * n + i];
+    const uint64_t lm = last < c.b.q ? last : mulmod_barrett(last, 1, c.b);
+    const uint64_t d = x >= lm ? x - lm : c.q - lm + x;
+    jb.out[e] = csub(shoup_lazy(d, c.inv, c.inv_s, c.q), c.q);
+  }
+}
+
+// m_l = c0_l + c1_l * s_l for the decrypted limbs l < nl (ciphertext.rs:332-341).
+__global__ void k_decrypt_dot(const DotJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
+                              const uint64_t* __restrict__ s, uint32_t n) {
+  const DotJob jb = jobs[blockIdx.y];
+  const uint32_t total = jb.nl * n;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const uint32_t l = e / n;
+    const BarrettConst m = bc[l];
+    jb.out[e] = addmod(jb.c0[e], mulmod_barrett(jb.c1[e], s[e], m), m.q);
+  }
+}
+
+static dim3 grid_for(uint32_t elems, uint32_t jobs) {
+  uint32_t bx = (elems + 255) / 256;
+  if (bx > 64) bx = 64;
+  return dim3(bx, jobs);
+}
+
+hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_limbs, const BarrettConst* bc,
+                            uint32_t n, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_ct_pt_mul, grid_for(2 * max_limbs * n, njobs), dim3(256), 0, s, jobs, bc, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
+                            uint32_t n, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_ct_addsub, grid_for(2 * max_limbs * n, njobs), dim3(256), 0, s, jobs, q, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_encrypt_prep(const EncPrepJob* jobs, uint32_t njobs, const BarrettConst* bc, uint32_t n,
+                               uint32_t L, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_encrypt_prep, grid_for(n, njobs), dim3(256), 0, s, jobs, bc, n, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
+                                  uint32_t n, uint32_t L, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_encrypt_combine, grid_for(L * n, njobs), dim3(256), 0, s, jobs, bc, n, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_rescale_combine(const RescaleJob* jobs, uint32_t njobs, const RescaleConst* rc, uint32_t n,
+                                  uint32_t L, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_rescale_combine, grid_for(2 * (L - 1) * n, njobs), dim3(256), 0, s, jobs, rc, n, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_decrypt_dot(const DotJob* jobs, uint32_t njobs, const BarrettConst* bc, const uint64_t* sk,
+                              uint32_t n, uint32_t max_nl, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  hipLaunchKernelGGL(k_decrypt_dot, grid_for(max_nl * n, njobs), dim3(256), 0, s, jobs, bc, sk, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_signed_to_rns(const int64_t* x, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
+                               hipStream_t s) {
+  hipLaunchKernelGGL(k_signed_to_rns, grid_for(n, 1), dim3(256), 0, s, x, dst, bc, n, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_sub_product(const uint64_t* x, const uint64_t* a, const uint64_t* sk, uint64_t* out,
+                              const BarrettConst* bc, uint32_t n, uint32_t L, hipStream_t s) {
+  hipLaunchKernelGGL(k_sub_product, grid_for(L * n, 1), dim3(256), 0, s, x, a, sk, out, bc, n, L);
+  return hipGetLastError();
+}
+
+}  // namespace th

@@ -1,0 +1,98 @@
+// Job descriptors and launchers of the element-wise and decode kernels.
+#pragma once
+#include "th_internal.h"
+
+namespace th {
+
+struct CtPtJob {
+  const uint64_t* ct0;  // component c0 (limbs x N)
+  const uint64_t* ct1;  // component c1
+  const uint64_t* pt;   // plaintext, NTT domain (>= limbs x N)
+  uint64_t* out;        // [c0 | c1], limbs x N each
+  uint32_t limbs;
+  uint32_t pad_;
+};
+
+struct AddJob {
+  const uint64_t* a;
+  const uint64_t* b;
+  uint64_t* out;
+  uint32_t limbs;
+  uint32_t sub;
+};
+
+struct EncPrepJob {
+  const int64_t* m;   // round(coeff * 2^40) per coefficient
+  const int64_t* e0;
+  const int64_t* e1;  // may be null (secret-key encryption)
+  const uint8_t* u;   // sample_ternary values {0,1,2}; may be null
+  uint64_t* dst;      // [M | E1 | U], L limb-polys each
+};
+
+struct EncCombineJob {
+  const uint64_t* prep;  // NTT of [M | E1 | U]
+  const uint64_t* pk_b;
+  const uint64_t* pk_a;
+  uint64_t* out;         // [c0 | c1]
+};
+
+struct RescaleConst {
+  uint64_t q, inv, inv_s;  // (q_last mod q)^{-1} and its Shoup companion
+  BarrettConst b;          // remainder of a 64-bit value modulo q
+};
+
+struct RescaleJob {
+  const uint64_t* coef;  // inverse-transformed input, [c0 | c1] with L limbs each
+  uint64_t* out;         // [c0 | c1] with L-1 limbs each (coefficient domain)
+};
+
+struct DotJob {
+  const uint64_t* c0;
+  const uint64_t* c1;
+  uint64_t* out;  // nl limb-polys
+  uint32_t nl;    // limbs to decrypt (1, or 2 for the CRT branch)
+  uint32_t pad_;
+};
+
+struct DecodeConst {
+  uint64_t q0, q1, half_q0;
+  uint64_t q0_inv_q1, q0_inv_q1_s;  // (q0 mod q1)^{-1} mod q1, Shoup companion
+  BarrettConst b1;                  // remainder modulo q1
+  uint64_t Q_lo, Q_hi, halfQ_lo, halfQ_hi;
+};
+
+struct DecodeJob {
+  const uint64_t* m;  // limb 0 (and limb 1 at m + N for the CRT branch), coefficient domain
+  double* parts;      // P parts x (re, im) x N/P doubles
+  double* out;        // N/2 decoded slots (may be null)
+  double* seg;        // cols segment sums (may be null)
+  double scale;
+  uint32_t crt;
+  uint32_t pad_;
+};
+
+hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_limbs, const BarrettConst* bc,
+                            uint32_t n, hipStream_t s);
+hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
+                            uint32_t n, hipStream_t s);
+hipError_t launch_encrypt_prep(const EncPrepJob* jobs, uint32_t njobs, const BarrettConst* bc, uint32_t n,
+                               uint32_t L, hipStream_t s);
+hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
+                                  uint32_t n, uint32_t L, hipStream_t s);
+hipError_t launch_rescale_combine(const RescaleJob* jobs, uint32_t njobs, const RescaleConst* rc, uint32_t n,
+                                  uint32_t L, hipStream_t s);
+hipError_t launch_decrypt_dot(const DotJob* jobs, uint32_t njobs, const BarrettConst* bc, const uint64_t* sk,
+                              uint32_t n, uint32_t max_nl, hipStream_t s);
+hipError_t launch_signed_to_rns(const int64_t* x, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
+                               hipStream_t s);
+hipError_t launch_sub_product(const uint64_t* x, const uint64_t* a, const uint64_t* sk, uint64_t* out,
+                              const BarrettConst* bc, uint32_t n, uint32_t L, hipStream_t s);
+// Decode (encoding.rs:219-239, :282-315) of njobs decrypted polynomials:
+// centring / CRT, twist, radix-2 DIT FFT and the real parts of the first N/2
+// outputs, optionally followed by sums over `cols` segments of d slots.
+hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* twist_re,
+                         const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
+                         uint32_t d, uint32_t cols, hipStream_t s);
+size_t decode_parts_doubles(uint32_t logn);  // scratch doubles per job
+
+}  // namespace th

@@ -1,0 +1,1284 @@
+// Host runtime of the CKKS engine and the implementation of the C ABI in
+// include/tensafe_he.h.
+//
+// A context owns: the per-limb NTT twiddle tables and constants in HBM, the
+// decode tables, one HIP stream, a size-bucketed device memory pool (buffers
+// are recycled in stream order, never returned to HIP until the context is
+// freed) and a pinned staging ring for host<->device traffic (job lists and
+// input vectors). Every operation is a short fixed pipeline of kernel
+// launches on the context stream; only calls that return host data wait.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <unordered_map>
+#include <vector>
+
+#include "host_math.h"
+#include "poly_kernels.h"
+#include "tensafe_he.h"
+
+using namespace th;
+
+namespace {
+
+thread_local std::string g_err = "";
+
+struct ThError : std::runtime_error {
+  int code;
+  ThError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void raise(int code, const std::string& m) { throw ThError(code, m); }
+
+void hipchk(hipError_t e, const char* what) {
+  if (e != hipSuccess) raise(TH_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPCHK(x) hipchk((x), #x)
+
+constexpr double kScale = 1099511627776.0;  // 2^40, params.rs:9-12
+
+// ---------------------------------------------------------------- memory
+class DevicePool {
+ public:
+  void* get(size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    std::lock_guard<std::mutex> lk(mu_);
+    auto& fl = free_[bytes];
+    if (!fl.empty()) {
+      void* p = fl.back();
+      fl.pop_back();
+      return p;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      raise(TH_ENOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    sizes_[p] = bytes;
+    return p;
+  }
+  void put(void* p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = sizes_.find(p);
+    if (it == sizes_.end()) return;
+    free_[it->second].push_back(p);
+  }
+  bool owns(void* p) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return sizes_.count(p) != 0;
+  }
+  void release_all() {
+    std::lock_guard<std::mutex> lk(mu_);
+    for (auto& kv : sizes_) (void)hipFree(kv.first);
+    sizes_.clear();
+    free_.clear();
+  }
+
+ private:
+  std::mutex mu_;
+  std::unordered_map<size_t, std::vector<void*>> free_;
+  std::unordered_map<void*, size_t> sizes_;
+};
+
+// Pinned host staging for host<->device copies. Allocation is a bump pointer;
+// when the ring is full the stream is drained first, so a region is never
+// rewritten while a queued copy may still read it. Device-side destinations
+// come from the pool through an OpScope (below), so nothing a queued kernel
+// reads is ever recycled before the kernels of the current call are queued.
+class StagingRing {
+ public:
+  void init(size_t bytes) {
+    cap_ = bytes;
+    HIPCHK(hipHostMalloc(&host_, cap_, hipHostMallocDefault));
+    off_ = 0;
+  }
+  void destroy() {
+    if (host_) (void)hipHostFree(host_);
+    host_ = nullptr;
+  }
+  void* reserve(size_t bytes, hipStream_t s) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    if (bytes > cap_) {
+      HIPCHK(hipStreamSynchronize(s));
+      destroy();
+      init(std::max(bytes, cap_ * 2));
+    } else if (off_ + bytes > cap_) {
+      HIPCHK(hipStreamSynchronize(s));
+      off_ = 0;
+    }
+    void* h = (char*)host_ + off_;
+    off_ += bytes;
+    return h;
+  }
+
+ private:
+  void* host_ = nullptr;
+  size_t cap_ = 0, off_ = 0;
+};
+
+// Parallel loop over independent host work items (sampling, encoding).
+template <class F>
+void parallel_for(size_t count, F&& f) {
+  size_t nt = std::min<size_t>(count, std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+  if (nt <= 1) {
+    for (size_t i = 0; i < count; ++i) f(i);
+    return;
+  }
+  std::vector<std::thread> ts;
+  std::vector<std::exception_ptr> errs(nt);
+  for (size_t t = 0; t < nt; ++t)
+    ts.emplace_back([&, t] {
+      try {
+        for (size_t i = t; i < count; i += nt) f(i);
+      } catch (...) {
+        errs[t] = std::current_exception();
+      }
+    });
+  for (auto& th : ts) th.join();
+  for (auto& e : errs)
+    if (e) std::rethrow_exception(e);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- handles
+struct th_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t N = 0, logn = 0, L = 0;
+  std::vector<uint64_t> q;
+  std::vector<LimbConst> h_lc;
+  LimbConst* d_lc = nullptr;
+  BarrettConst* d_bc = nullptr;
+  uint64_t* d_q = nullptr;
+  RescaleConst* d_rc = nullptr;  // [level][l], level = input limb count (2..L), row stride L
+  DecodeConst* d_dc = nullptr;
+  double *d_twist_re = nullptr, *d_twist_im = nullptr, *d_stage_re = nullptr, *d_stage_im = nullptr;
+  void* d_tables = nullptr;  // twiddle storage
+  Encoder enc;
+  DevicePool pool;
+  StagingRing ring;
+  std::mutex mu;
+};
+
+struct th_sk {
+  th_ctx* ctx;
+  uint64_t* d;  // L x N, NTT domain
+};
+struct th_pk {
+  th_ctx* ctx;
+  uint64_t* d;  // [b | a], L x N each
+};
+struct th_ct {
+  th_ctx* ctx;
+  uint32_t limbs;
+  double scale;
+  uint64_t* d;  // [c0 | c1], limbs x N each
+};
+struct th_pt {
+  th_ctx* ctx;
+  uint32_t limbs;
+  uint64_t* d;  // limbs x N
+};
+
+namespace {
+
+// Device buffers used by one API call (job lists, uploaded inputs, scratch).
+// They go back to the pool when the call returns, after all of its kernels
+// are queued; the next user of a recycled buffer is ordered after them on
+// the same stream.
+struct OpScope {
+  th_ctx* c;
+  std::vector<void*> bufs;
+  explicit OpScope(th_ctx* ctx) : c(ctx) {}
+  ~OpScope() {
+    for (void* p : bufs) c->pool.put(p);
+  }
+  OpScope(const OpScope&) = delete;
+  OpScope& operator=(const OpScope&) = delete;
+  void* dev(size_t bytes) {
+    void* p = c->pool.get(bytes);
+    bufs.push_back(p);
+    return p;
+  }
+  void* upload(const void* src, size_t bytes) {
+    void* h = c->ring.reserve(bytes, c->stream);
+    memcpy(h, src, bytes);
+    void* d = dev(bytes);
+    HIPCHK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, c->stream));
+    return d;
+  }
+  template <class T>
+  T* up(const std::vector<T>& v) {
+    return (T*)upload(v.data(), v.size() * sizeof(T));
+  }
+};
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    return TH_OK;
+  } catch (const ThError& e) {
+    g_err = e.what();
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_err = "host allocation failed";
+    return TH_ENOMEM;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return TH_EINVAL;
+  } catch (...) {
+    g_err = "unknown error";
+    return TH_EINVAL;
+  }
+}
+
+void need(bool cond, const std::string& msg, int code = TH_EINVAL) {
+  if (!cond) raise(code, msg);
+}
+
+void use_device(th_ctx* c) { HIPCHK(hipSetDevice(c->device)); }
+
+size_t poly_bytes(const th_ctx* c) { return (size_t)c->N * 8; }
+
+th_ct* new_ct(th_ctx* c, uint32_t limbs, double scale) {
+  th_ct* ct = new th_ct{c, limbs, scale, nullptr};
+  ct->d = (uint64_t*)c->pool.get(2 * limbs * poly_bytes(c));
+  return ct;
+}
+
+void check_ct(th_ctx* c, const th_ct* ct) {
+  need(ct != nullptr, "null ciphertext");
+  need(ct->ctx == c, "ciphertext belongs to another context");
+}
+
+// ---------------------------------------------------------------- NTT dispatch
+void ntt_strided(th_ctx* c, bool inverse, const uint64_t* src, uint64_t* dst, uint32_t njobs, uint32_t limb_mod,
+                 uint32_t limb_base = 0) {
+  NttArgs a{};
+  a.lc = c->d_lc;
+  a.jobs = nullptr;
+  a.src = src;
+  a.dst = dst;
+  a.stride = c->N;
+  a.limb_mod = limb_mod;
+  a.limb_base = limb_base;
+  HIPCHK(launch_ntt((int)c->logn, inverse, a, njobs, c->stream));
+}
+
+void ntt_list(OpScope& sc, bool inverse, const std::vector<NttJob>& jobs) {
+  th_ctx* c = sc.c;
+  if (jobs.empty()) return;
+  NttArgs a{};
+  a.lc = c->d_lc;
+  a.jobs = sc.up(jobs);
+  HIPCHK(launch_ntt((int)c->logn, inverse, a, (uint32_t)jobs.size(), c->stream));
+}
+
+// ---------------------------------------------------------------- context setup
+void build_tables(th_ctx* c) {
+  const uint32_t N = c->N, L = c->L;
+  std::vector<BarrettConst> bc(L);
+  c->h_lc.resize(L);
+  // twiddles: per limb forward then inverse, N pairs of 16 bytes each
+  const size_t tab_bytes = (size_t)L * 2 * N * 16;
+  HIPCHK(hipMalloc(&c->d_tables, tab_bytes));
+  std::vector<uint64_t> fw(N), iw(N);
+  std::vector<unsigned char> host_tab(tab_bytes);
+  for (uint32_t l = 0; l < L; ++l) {
+    const uint64_t q = c->q[l];
+    const uint64_t psi = primitive_2n_root(N, q);
+    need(psi != 0, "no primitive 2N-th root of unity for q=" + std::to_string(q));
+    const uint64_t psi_inv = invmod(psi, q);
+    uint64_t p = 1, pi = 1;
+    for (uint32_t i = 0; i < N; ++i) {  // fwd[brv(i)] = psi^i, inv[brv(i)] = psi^-i (rns.rs:161-185)
+      const uint32_t r = __builtin_bitreverse32(i) >> (32 - c->logn);
+      fw[r] = p;
+      iw[r] = pi;
+      p = (uint64_t)(((u128)p * psi) % q);
+      pi = (uint64_t)(((u128)pi * psi_inv) % q);
+    }
+    const bool fp = q < FP64_PRIME_LIMIT;
+    unsigned char* fdst = host_tab.data() + (size_t)(2 * l) * N * 16;
+    unsigned char* idst = host_tab.data() + (size_t)(2 * l + 1) * N * 16;
+    for (uint32_t i = 0; i < N; ++i) {
+      if (fp) {
+        Fp64Tw a{(double)fw[i], (double)fw[i] / (double)q}, b{(double)iw[i], (double)iw[i] / (double)q};
+        memcpy(fdst + 16 * (size_t)i, &a, 16);
+        memcpy(idst + 16 * (size_t)i, &b, 16);
+      } else {
+        ShoupTw a{fw[i], (uint64_t)(((u128)fw[i] << 64) / q)}, b{iw[i], (uint64_t)(((u128)iw[i] << 64) / q)};
+        memcpy(fdst + 16 * (size_t)i, &a, 16);
+        memcpy(idst + 16 * (size_t)i, &b, 16);
+      }
+    }
+    LimbConst& lc = c->h_lc[l];
+    memset(&lc, 0, sizeof(lc));
+    lc.q = q;
+    lc.two_q = 2 * q;
+    lc.n_inv = invmod(N % q, q);
+    lc.n_inv_s = (uint64_t)(((u128)lc.n_inv << 64) / q);
+    lc.last_w = (uint64_t)(((u128)iw[1] * lc.n_inv) % q);
+    lc.last_ws = (uint64_t)(((u128)lc.last_w << 64) / q);
+    lc.qd = (double)q;
+    lc.qinv = 1.0 / (double)q;
+    lc.n_inv_d = (double)lc.n_inv;
+    lc.n_inv_dq = (double)lc.n_inv / (double)q;
+    lc.last_wd = (double)lc.last_w;
+    lc.last_wdq = (double)lc.last_w / (double)q;
+    lc.fwd = (const char*)c->d_tables + (size_t)(2 * l) * N * 16;
+    lc.inv = (const char*)c->d_tables + (size_t)(2 * l + 1) * N * 16;
+    lc.fp64 = fp ? 1 : 0;
+    const u128 r = (~(u128)0) / q;
+    bc[l] = BarrettConst{q, (uint64_t)(r >> 64), (uint64_t)r};
+  }
+  HIPCHK(hipMemcpy(c->d_tables, host_tab.data(), tab_bytes, hipMemcpyHostToDevice));
+  HIPCHK(hipMalloc(&c->d_lc, L * sizeof(LimbConst)));
+  HIPCHK(hipMemcpy(c->d_lc, c->h_lc.data(), L * sizeof(LimbConst), hipMemcpyHostToDevice));
+  HIPCHK(hipMalloc(&c->d_bc, L * sizeof(BarrettConst)));
+  HIPCHK(hipMemcpy(c->d_bc, bc.data(), L * sizeof(BarrettConst), hipMemcpyHostToDevice));
+  HIPCHK(hipMalloc(&c->d_q, L * 8));
+  HIPCHK(hipMemcpy(c->d_q, c->q.data(), L * 8, hipMemcpyHostToDevice));
+
+  // rescale constants (ciphertext.rs:496-497)
+  std::vector<RescaleConst> rc((size_t)(L + 1) * L);
+  for (uint32_t lev = 2; lev <= L; ++lev) {
+    const uint64_t qlast = c->q[lev - 1];
+    for (uint32_t l = 0; l + 1 < lev; ++l) {
+      const uint64_t q = c->q[l];
+      RescaleConst& x = rc[(size_t)lev * L + l];
+      x.q = q;
+      x.inv = invmod(qlast % q, q);
+      x.inv_s = (uint64_t)(((u128)x.inv << 64) / q);
+      x.b = bc[l];
+    }
+  }
+  HIPCHK(hipMalloc(&c->d_rc, rc.size() * sizeof(RescaleConst)));
+  HIPCHK(hipMemcpy(c->d_rc, rc.data(), rc.size() * sizeof(RescaleConst), hipMemcpyHostToDevice));
+
+  // decode constants (encoding.rs:221-233, ciphertext.rs:352-390)
+  DecodeConst dc;
+  memset(&dc, 0, sizeof(dc));
+  dc.q0 = c->q[0];
+  dc.half_q0 = c->q[0] / 2;
+  if (L >= 2) {
+    dc.q1 = c->q[1];
+    dc.q0_inv_q1 = invmod(c->q[0] % c->q[1], c->q[1]);
+    dc.q0_inv_q1_s = (uint64_t)(((u128)dc.q0_inv_q1 << 64) / c->q[1]);
+    dc.b1 = bc[1];
+    const u128 Q = (u128)c->q[0] * c->q[1], h = Q / 2;
+    dc.Q_lo = (uint64_t)Q;
+    dc.Q_hi = (uint64_t)(Q >> 64);
+    dc.halfQ_lo = (uint64_t)h;
+    dc.halfQ_hi = (uint64_t)(h >> 64);
+  }
+  HIPCHK(hipMalloc(&c->d_dc, sizeof(DecodeConst)));
+  HIPCHK(hipMemcpy(c->d_dc, &dc, sizeof(dc), hipMemcpyHostToDevice));
+
+  c->enc.init(N);
+  HIPCHK(hipMalloc(&c->d_twist_re, N * 8));
+  HIPCHK(hipMalloc(&c->d_twist_im, N * 8));
+  HIPCHK(hipMalloc(&c->d_stage_re, N * 8));
+  HIPCHK(hipMalloc(&c->d_stage_im, N * 8));
+  HIPCHK(hipMemcpy(c->d_twist_re, c->enc.twist_re.data(), N * 8, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d_twist_im, c->enc.twist_im.data(), N * 8, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d_stage_re, c->enc.stage_re.data(), N * 8, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->d_stage_im, c->enc.stage_im.data(), N * 8, hipMemcpyHostToDevice));
+}
+
+void destroy_ctx(th_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  c->pool.release_all();
+  c->ring.destroy();
+  void* bufs[] = {c->d_lc, c->d_bc, c->d_q, c->d_rc, c->d_dc, c->d_twist_re, c->d_twist_im,
+                  c->d_stage_re, c->d_stage_im, c->d_tables};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+// ---------------------------------------------------------------- host-side inputs
+void pad_input(const th_ctx* c, const double* z, size_t n, std::vector<double>& out) {
+  // lib.rs:123-126: pad or truncate to N/2 slots
+  const size_t S = c->N / 2;
+  out.assign(S, 0.0);
+  const size_t m = std::min(n, S);
+  if (m) memcpy(out.data(), z, m * 8);
+}
+
+// Upload signed coefficients and reduce them into L limb-polys at dst.
+void upload_signed(OpScope& sc, const std::vector<int64_t>& x, uint64_t* dst, uint32_t limbs) {
+  th_ctx* c = sc.c;
+  const int64_t* d = sc.up(x);
+  HIPCHK(launch_signed_to_rns(d, dst, c->d_bc, c->N, limbs, c->stream));
+}
+
+// encrypt_pk for `count` inputs with host-drawn or caller-supplied randomness.
+struct PkInput {
+  std::vector<int64_t> m, e0, e1;
+  std::vector<uint8_t> u;
+};
+
+void encrypt_pk_inputs(th_ctx* c, const th_pk* pk, std::vector<PkInput>& in, th_ct** outs) {
+  const uint32_t N = c->N, L = c->L;
+  const size_t count = in.size();
+  OpScope sc(c);
+  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
+  std::vector<EncPrepJob> pj(count);
+  for (size_t i = 0; i < count; ++i) {
+    pj[i].m = sc.up(in[i].m);
+    pj[i].e0 = sc.up(in[i].e0);
+    pj[i].e1 = sc.up(in[i].e1);
+    pj[i].u = sc.up(in[i].u);
+    pj[i].dst = prep + i * 3 * L * N;
+  }
+  HIPCHK(launch_encrypt_prep(sc.up(pj), (uint32_t)count, c->d_bc, N, L, c->stream));
+  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
+  std::vector<EncCombineJob> cj(count);
+  std::vector<th_ct*> made;
+  try {
+    for (size_t i = 0; i < count; ++i) {
+      th_ct* ct = new_ct(c, L, kScale);  // ciphertext.rs:314-318
+      made.push_back(ct);
+      cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, ct->d};
+    }
+    HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
+  } catch (...) {
+    for (th_ct* ct : made) {
+      c->pool.put(ct->d);
+      delete ct;
+    }
+    throw;
+  }
+  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+}
+
+void draw_pk_randomness(uint64_t seed, int has_seed, uint32_t N, PkInput& x) {
+  ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
+  // ciphertext.rs:255-273: u, then e0, then e1
+  x.u.resize(N);
+  x.e0.resize(N);
+  x.e1.resize(N);
+  draw_ternary(s, N, x.u.data());
+  draw_gaussian(s, N, x.e0.data());
+  draw_gaussian(s, N, x.e1.data());
+}
+
+// ---------------------------------------------------------------- decryption pipeline
+// Queue decrypt + decode of `count` ciphertexts; slots to out_dev (count x S) and/or
+// segment sums to seg_dev (count x cols). Scratch lives in the caller's scope.
+void queue_decrypt(OpScope& sc, const th_ct* const* cts, size_t count, const th_sk* sk, double* out_dev,
+                   double* seg_dev, uint32_t d, uint32_t cols) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, S = N / 2;
+  uint64_t* dot = (uint64_t*)sc.dev(count * 2 * poly_bytes(c));
+  double* parts = (double*)sc.dev(count * decode_parts_doubles(c->logn) * 8);
+  std::vector<DotJob> dj(count);
+  std::vector<NttJob> nj;
+  std::vector<DecodeJob> dec(count);
+  uint32_t max_nl = 1;
+  for (size_t i = 0; i < count; ++i) {
+    const th_ct* ct = cts[i];
+    // ciphertext.rs:351: CRT branch iff scale > 1.5 * 2^40 and at least two limbs
+    const uint32_t nl = (ct->scale > kScale * 1.5 && ct->limbs >= 2) ? 2 : 1;
+    max_nl = std::max(max_nl, nl);
+    uint64_t* o = dot + i * 2 * N;
+    dj[i] = DotJob{ct->d, ct->d + (size_t)ct->limbs * N, o, nl, 0};
+    for (uint32_t l = 0; l < nl; ++l) nj.push_back(NttJob{o + (size_t)l * N, o + (size_t)l * N, l, 0});
+    dec[i].m = o;
+    dec[i].parts = parts + i * decode_parts_doubles(c->logn);
+    dec[i].out = out_dev ? out_dev + i * S : nullptr;
+    dec[i].seg = seg_dev ? seg_dev + i * cols : nullptr;
+    dec[i].scale = ct->scale;
+    dec[i].crt = nl == 2;
+  }
+  HIPCHK(launch_decrypt_dot(sc.up(dj), (uint32_t)count, c->d_bc, sk->d, N, max_nl, c->stream));
+  ntt_list(sc, true, nj);
+  HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
+                       c->d_stage_im, c->logn, d, cols, c->stream));
+}
+
+void check_decrypt_args(th_ctx* c, const th_ct* const* cts, size_t count, const th_sk* sk) {
+  need(sk && sk->ctx == c, "secret key belongs to another context");
+  need(cts != nullptr || count == 0, "null ciphertext list");
+  for (size_t i = 0; i < count; ++i) check_ct(c, cts[i]);
+}
+
+// D2H through the staging ring, then wait.
+void download(th_ctx* c, void* dst, const void* src_dev, size_t bytes) {
+  void* h = c->ring.reserve(bytes, c->stream);
+  HIPCHK(hipMemcpyAsync(h, src_dev, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipStreamSynchronize(c->stream));
+  memcpy(dst, h, bytes);
+}
+
+void rescale_many(th_ctx* c, const th_ct* const* cts, size_t count, th_ct** outs) {
+  const uint32_t N = c->N;
+  const uint32_t L = cts[0]->limbs;
+  for (size_t i = 0; i < count; ++i) {
+    check_ct(c, cts[i]);
+    need(cts[i]->limbs == L, "rescale_batch: all ciphertexts must have the same limb count");
+  }
+  need(L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);  // ciphertext.rs:479
+  OpScope sc(c);
+  uint64_t* coef = (uint64_t*)sc.dev(count * 2 * L * poly_bytes(c));
+  std::vector<NttJob> inv;
+  inv.reserve(count * 2 * L);
+  std::vector<th_ct*> made;
+  std::vector<RescaleJob> rj(count);
+  try {
+    for (size_t i = 0; i < count; ++i)
+      for (uint32_t k = 0; k < 2 * L; ++k)
+        inv.push_back(NttJob{cts[i]->d + (size_t)k * N, coef + (i * 2 * L + k) * N, k % L, 0});
+    ntt_list(sc, true, inv);
+    for (size_t i = 0; i < count; ++i) {
+      th_ct* o = new_ct(c, L - 1, cts[i]->scale / (double)c->q[L - 1]);  // ciphertext.rs:533
+      made.push_back(o);
+      rj[i] = RescaleJob{coef + i * 2 * L * N, o->d};
+    }
+    HIPCHK(launch_rescale_combine(sc.up(rj), (uint32_t)count, c->d_rc + (size_t)L * c->L, N, L, c->stream));
+    std::vector<NttJob> fwd;
+    fwd.reserve(count * 2 * (L - 1));
+    for (size_t i = 0; i < count; ++i)
+      for (uint32_t k = 0; k < 2 * (L - 1); ++k)
+        fwd.push_back(NttJob{made[i]->d + (size_t)k * N, made[i]->d + (size_t)k * N, k % (L - 1), 0});
+    ntt_list(sc, false, fwd);
+  } catch (...) {
+    for (th_ct* o : made) {
+      c->pool.put(o->d);
+      delete o;
+    }
+    throw;
+  }
+  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+}
+
+th_pt* encode_pt(th_ctx* c, const double* z, size_t n) {
+  std::vector<double> pad;
+  pad_input(c, z, n, pad);
+  std::vector<int64_t> m(c->N);
+  c->enc.encode_i64(pad.data(), pad.size(), m.data());
+  th_pt* pt = new th_pt{c, c->L, (uint64_t*)c->pool.get(c->L * poly_bytes(c))};
+  OpScope sc(c);
+  upload_signed(sc, m, pt->d, c->L);
+  ntt_strided(c, false, pt->d, pt->d, c->L, c->L);
+  return pt;
+}
+
+void ct_pt_many(th_ctx* c, const th_ct* const* cts, const th_pt* const* pts, size_t count, th_ct** outs) {
+  std::vector<CtPtJob> jobs(count);
+  std::vector<th_ct*> made;
+  uint32_t maxl = 1;
+  try {
+    for (size_t i = 0; i < count; ++i) {
+      check_ct(c, cts[i]);
+      need(pts[i] && pts[i]->ctx == c, "plaintext belongs to another context");
+      need(pts[i]->limbs >= cts[i]->limbs, "plaintext has fewer limbs than the ciphertext");
+      th_ct* o = new_ct(c, cts[i]->limbs, cts[i]->scale * cts[i]->scale);  // ciphertext.rs:427
+      made.push_back(o);
+      const size_t ln = (size_t)cts[i]->limbs * c->N;
+      jobs[i] = CtPtJob{cts[i]->d, cts[i]->d + ln, pts[i]->d, o->d, cts[i]->limbs, 0};
+      maxl = std::max(maxl, cts[i]->limbs);
+    }
+    OpScope sc(c);
+    HIPCHK(launch_ct_pt_mul(sc.up(jobs), (uint32_t)count, maxl, c->d_bc, c->N, c->stream));
+  } catch (...) {
+    for (th_ct* o : made) {
+      c->pool.put(o->d);
+      delete o;
+    }
+    throw;
+  }
+  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+}
+
+void add_sub(th_ctx* c, const th_ct* a, const th_ct* b, bool sub, th_ct** out) {
+  check_ct(c, a);
+  check_ct(c, b);
+  // ciphertext.rs:436-441
+  need(fabs(a->scale - b->scale) < 1.0, std::string("Scale mismatch in ") + (sub ? "ct_sub" : "ct_add"));
+  need(a->limbs == b->limbs, "limb count mismatch");
+  th_ct* o = new_ct(c, a->limbs, a->scale);
+  AddJob j{a->d, b->d, o->d, a->limbs, sub ? 1u : 0u};
+  try {
+    OpScope sc(c);
+    HIPCHK(launch_ct_addsub(sc.up(std::vector<AddJob>{j}), 1, a->limbs, c->d_q, c->N, c->stream));
+  } catch (...) {
+    c->pool.put(o->d);
+    delete o;
+    throw;
+  }
+  *out = o;
+}
+
+void ntt_batch(th_ctx* c, uint64_t* polys, size_t count, uint32_t limbs, int on_device, bool inverse) {
+  need(limbs >= 1 && limbs <= c->L, "limbs must be in [1, L]");
+  const size_t bytes = count * limbs * poly_bytes(c);
+  if (!count) return;
+  if (on_device) {
+    ntt_strided(c, inverse, polys, polys, (uint32_t)(count * limbs), limbs);
+    return;
+  }
+  OpScope sc(c);
+  uint64_t* d = (uint64_t*)sc.upload(polys, bytes);
+  ntt_strided(c, inverse, d, d, (uint32_t)(count * limbs), limbs);
+  download(c, polys, d, bytes);
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+extern "C" {
+
+const char* th_last_error(void) { return g_err.c_str(); }
+const char* th_version(void) { return "tensafe-he-mi355x 0.1.0 (gfx950)"; }
+
+int th_device_count(int* count) {
+  return guarded([&] {
+    need(count != nullptr, "null output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    *count = n;
+  });
+}
+
+int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale_bits, int device, th_ctx** out) {
+  return guarded([&] {
+    need(out != nullptr, "null output");
+    *out = nullptr;
+    need(N >= (1u << NTT_MIN_LOGN) && N <= (1u << NTT_MAX_LOGN) && (N & (N - 1)) == 0,
+         "Unsupported poly_mod_degree: " + std::to_string(N) + ". Use a power of two in [1024, 32768].");
+    need(scale_bits == 40, "scale_bits must be 40");
+    std::vector<uint64_t> q;
+    if (moduli) {
+      need(L >= 1 && L <= 16, "L must be in [1, 16]");
+      q.assign(moduli, moduli + L);
+      for (uint32_t i = 0; i < L; ++i) {
+        need(q[i] < (1ULL << 62), "moduli must be below 2^62");
+        need(q[i] % (2ULL * N) == 1, "modulus " + std::to_string(q[i]) + " is not 1 mod 2N");
+        need(is_prime(q[i]), "modulus " + std::to_string(q[i]) + " is not prime");
+        for (uint32_t j = 0; j < i; ++j) need(q[i] != q[j], "moduli must be distinct");
+      }
+    } else {
+      need(default_chain(N, q), "Unsupported poly_mod_degree: " + std::to_string(N) +
+                                    ". Use 8192, 16384, or 32768.");  // lib.rs:38-47
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+      (void)hipGetLastError();
+      raise(TH_EDEVICE, "no HIP device available (the tensafe_he engine requires an MI355X / gfx950 GPU)");
+    }
+    need(device >= 0 && device < ndev, "device index out of range", TH_EDEVICE);
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      raise(TH_EDEVICE, std::string("device is ") + prop.gcnArchName + ", the engine is built for gfx950");
+    th_ctx* c = new th_ctx();
+    try {
+      c->device = device;
+      c->N = N;
+      c->logn = (uint32_t)__builtin_ctz(N);
+      c->L = (uint32_t)q.size();
+      c->q = q;
+      HIPCHK(hipSetDevice(device));
+      HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      build_tables(c);
+      c->ring.init(64u << 20);
+    } catch (...) {
+      destroy_ctx(c);
+      throw;
+    }
+    *out = c;
+  });
+}
+
+int th_ctx_free(th_ctx* ctx) {
+  return guarded([&] { destroy_ctx(ctx); });
+}
+
+int th_ctx_info(const th_ctx* ctx, uint32_t* N, uint32_t* L, uint64_t* moduli_out) {
+  return guarded([&] {
+    need(ctx != nullptr, "null context");
+    if (N) *N = ctx->N;
+    if (L) *L = ctx->L;
+    if (moduli_out) memcpy(moduli_out, ctx->q.data(), ctx->L * 8);
+  });
+}
+
+int th_ctx_sync(th_ctx* ctx) {
+  return guarded([&] {
+    need(ctx != nullptr, "null context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    use_device(ctx);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int th_ctx_stream(th_ctx* ctx, void** stream) {
+  return guarded([&] {
+    need(ctx && stream, "null argument");
+    *stream = (void*)ctx->stream;
+  });
+}
+
+#define TH_LOCK(c)                          \
+  need((c) != nullptr, "null context");     \
+  std::lock_guard<std::mutex> _lk((c)->mu); \
+  use_device(c)
+
+int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    const uint32_t N = ctx->N, L = ctx->L;
+    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
+    std::vector<uint8_t> t(N);
+    draw_ternary(s, N, t.data());  // ciphertext.rs:86
+    std::vector<int64_t> v(N);
+    for (uint32_t i = 0; i < N; ++i) v[i] = t[i] == 0 ? -1 : (t[i] == 1 ? 0 : 1);  // ciphertext.rs:91-96
+    th_sk* sk = new th_sk{ctx, (uint64_t*)ctx->pool.get(L * poly_bytes(ctx))};
+    OpScope sc(ctx);
+    upload_signed(sc, v, sk->d, L);
+    ntt_strided(ctx, false, sk->d, sk->d, L, L);
+    *out = sk;
+  });
+}
+
+int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, th_pk** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr && sk != nullptr && sk->ctx == ctx, "bad secret key");
+    const uint32_t N = ctx->N, L = ctx->L;
+    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
+    // ciphertext.rs:119-127: a for every limb, then e
+    std::vector<uint64_t> a((size_t)L * N);
+    for (uint32_t l = 0; l < L; ++l)
+      for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
+    std::vector<int64_t> e(N);
+    draw_gaussian(s, N, e.data());
+    th_pk* pk = new th_pk{ctx, (uint64_t*)ctx->pool.get(2 * L * poly_bytes(ctx))};
+    uint64_t* b = pk->d;
+    uint64_t* ad = pk->d + (size_t)L * N;
+    OpScope sc(ctx);
+    uint64_t* etmp = (uint64_t*)sc.dev(L * poly_bytes(ctx));
+    const uint64_t* a_up = sc.up(a);
+    HIPCHK(hipMemcpyAsync(ad, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    upload_signed(sc, e, etmp, L);
+    ntt_strided(ctx, false, ad, ad, L, L);
+    ntt_strided(ctx, false, etmp, etmp, L, L);
+    HIPCHK(launch_sub_product(etmp, ad, sk->d, b, ctx->d_bc, N, L, ctx->stream));  // b = e - a*s
+    *out = pk;
+  });
+}
+
+int th_sk_free(th_sk* sk) {
+  return guarded([&] {
+    if (!sk) return;
+    sk->ctx->pool.put(sk->d);
+    delete sk;
+  });
+}
+
+int th_pk_free(th_pk* pk) {
+  return guarded([&] {
+    if (!pk) return;
+    pk->ctx->pool.put(pk->d);
+    delete pk;
+  });
+}
+
+int th_sk_download(th_ctx* ctx, const th_sk* sk, uint64_t* out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(sk && sk->ctx == ctx && out, "bad argument");
+    download(ctx, out, sk->d, ctx->L * poly_bytes(ctx));
+  });
+}
+
+int th_pk_download(th_ctx* ctx, const th_pk* pk, uint64_t* b, uint64_t* a) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(pk && pk->ctx == ctx && b && a, "bad argument");
+    const size_t bytes = ctx->L * poly_bytes(ctx);
+    download(ctx, b, pk->d, bytes);
+    download(ctx, a, pk->d + (size_t)ctx->L * ctx->N, bytes);
+  });
+}
+
+}  // extern "C"
+
+namespace {
+// Secret-key encryption of one padded input with randomness from `s`
+// (ciphertext.rs:167-229: encode, a for every limb, then e).
+th_ct* encrypt_sk_one(th_ctx* ctx, const th_sk* sk, const std::vector<double>& pad, ChaChaStream& s) {
+  const uint32_t N = ctx->N, L = ctx->L;
+  std::vector<int64_t> m(N);
+  ctx->enc.encode_i64(pad.data(), pad.size(), m.data());
+  std::vector<uint64_t> a((size_t)L * N);
+  for (uint32_t l = 0; l < L; ++l)
+    for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
+  std::vector<int64_t> e(N);
+  draw_gaussian(s, N, e.data());
+  th_ct* ct = new_ct(ctx, L, kScale);
+  uint64_t* c0 = ct->d;
+  uint64_t* c1 = ct->d + (size_t)L * N;
+  try {
+    OpScope sc(ctx);
+    uint64_t* me = (uint64_t*)sc.dev(L * poly_bytes(ctx));
+    EncPrepJob pj{sc.up(m), sc.up(e), nullptr, nullptr, me};
+    HIPCHK(launch_encrypt_prep(sc.up(std::vector<EncPrepJob>{pj}), 1, ctx->d_bc, N, L, ctx->stream));
+    const uint64_t* a_up = sc.up(a);
+    HIPCHK(hipMemcpyAsync(c1, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    ntt_strided(ctx, false, me, me, L, L);
+    ntt_strided(ctx, false, c1, c1, L, L);
+    HIPCHK(launch_sub_product(me, c1, sk->d, c0, ctx->d_bc, N, L, ctx->stream));  // c0 = (m + e) - a*s
+  } catch (...) {
+    ctx->pool.put(ct->d);
+    delete ct;
+    throw;
+  }
+  return ct;
+}
+}  // namespace
+
+extern "C" {
+
+int th_encrypt(th_ctx* ctx, const th_sk* sk, const double* z, size_t n, uint64_t seed, int has_seed, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && sk && sk->ctx == ctx, "bad argument");
+    need(z != nullptr || n == 0, "null input");
+    std::vector<double> pad;
+    pad_input(ctx, z, n, pad);
+    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
+    *out = encrypt_sk_one(ctx, sk, pad, s);
+  });
+}
+
+int th_encrypt_batch(th_ctx* ctx, const th_sk* sk, const double* z, const uint64_t* lens, size_t stride,
+                     size_t count, uint64_t seed, int has_seed, th_ct** outs) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(outs && sk && sk->ctx == ctx && (count == 0 || (z && lens)), "bad argument");
+    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();  // lib.rs:238-241
+    std::vector<th_ct*> made;
+    try {
+      for (size_t i = 0; i < count; ++i) {
+        std::vector<double> pad;
+        pad_input(ctx, z + i * stride, (size_t)lens[i], pad);
+        made.push_back(encrypt_sk_one(ctx, sk, pad, s));
+      }
+    } catch (...) {
+      for (th_ct* ct : made) {
+        ctx->pool.put(ct->d);
+        delete ct;
+      }
+      throw;
+    }
+    for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+  });
+}
+
+int th_encrypt_pk(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, uint64_t seed, int has_seed, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && pk && pk->ctx == ctx, "bad argument");
+    need(z != nullptr || n == 0, "null input");
+    std::vector<PkInput> in(1);
+    std::vector<double> pad;
+    pad_input(ctx, z, n, pad);
+    in[0].m.resize(ctx->N);
+    ctx->enc.encode_i64(pad.data(), pad.size(), in[0].m.data());
+    draw_pk_randomness(seed, has_seed, ctx->N, in[0]);
+    encrypt_pk_inputs(ctx, pk, in, out);
+  });
+}
+
+int th_encrypt_pk_explicit(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, const uint8_t* u,
+                           const int64_t* e0, const int64_t* e1, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && pk && pk->ctx == ctx && u && e0 && e1, "bad argument");
+    need(z != nullptr || n == 0, "null input");
+    const uint32_t N = ctx->N;
+    for (uint32_t i = 0; i < N; ++i) need(u[i] <= 2, "u values must be in {0, 1, 2}");
+    std::vector<PkInput> in(1);
+    std::vector<double> pad;
+    pad_input(ctx, z, n, pad);
+    in[0].m.resize(N);
+    ctx->enc.encode_i64(pad.data(), pad.size(), in[0].m.data());
+    in[0].u.assign(u, u + N);
+    in[0].e0.assign(e0, e0 + N);
+    in[0].e1.assign(e1, e1 + N);
+    encrypt_pk_inputs(ctx, pk, in, out);
+  });
+}
+
+int th_encrypt_pk_batch(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, size_t stride, size_t count,
+                        const uint64_t* seeds, th_ct** outs) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(outs && pk && pk->ctx == ctx && seeds, "bad argument");
+    need(z != nullptr || count == 0, "null input");
+    if (!count) return;
+    std::vector<PkInput> in(count);
+    parallel_for(count, [&](size_t i) {
+      std::vector<double> pad;
+      pad_input(ctx, z + i * stride, n, pad);
+      in[i].m.resize(ctx->N);
+      ctx->enc.encode_i64(pad.data(), pad.size(), in[i].m.data());
+      draw_pk_randomness(seeds[i], 1, ctx->N, in[i]);
+    });
+    encrypt_pk_inputs(ctx, pk, in, outs);
+  });
+}
+
+int th_encode_to_ntt(th_ctx* ctx, const double* z, size_t n, th_pt** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && (z || n == 0), "bad argument");
+    need(n <= ctx->N / 2, "Input length exceeds slot count");  // encoding.rs:174-179
+    *out = encode_pt(ctx, z, n);
+  });
+}
+
+int th_pt_free(th_pt* pt) {
+  return guarded([&] {
+    if (!pt) return;
+    pt->ctx->pool.put(pt->d);
+    delete pt;
+  });
+}
+
+int th_pt_download(th_ctx* ctx, const th_pt* pt, uint64_t* out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(pt && pt->ctx == ctx && out, "bad argument");
+    download(ctx, out, pt->d, pt->limbs * poly_bytes(ctx));
+  });
+}
+
+int th_ct_pt_mul(th_ctx* ctx, const th_ct* ct, const double* pt, size_t n, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && (pt || n == 0), "bad argument");
+    check_ct(ctx, ct);
+    th_pt* p = encode_pt(ctx, pt, n);  // lib.rs:184-187 pads/truncates to N/2
+    try {
+      const th_ct* cs[1] = {ct};
+      const th_pt* ps[1] = {p};
+      ct_pt_many(ctx, cs, ps, 1, out);
+    } catch (...) {
+      ctx->pool.put(p->d);
+      delete p;
+      throw;
+    }
+    ctx->pool.put(p->d);
+    delete p;
+  });
+}
+
+int th_ct_pt_mul_ntt(th_ctx* ctx, const th_ct* ct, const th_pt* pt, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    const th_ct* cs[1] = {ct};
+    const th_pt* ps[1] = {pt};
+    ct_pt_many(ctx, cs, ps, 1, out);
+  });
+}
+
+int th_ct_pt_mul_ntt_batch(th_ctx* ctx, const th_ct* const* cts, const th_pt* const* pts, size_t count,
+                           th_ct** outs) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(outs && ((cts && pts) || count == 0), "bad argument");
+    if (count) ct_pt_many(ctx, cts, pts, count, outs);
+  });
+}
+
+int th_ct_add(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    add_sub(ctx, a, b, false, out);
+  });
+}
+
+int th_ct_sub(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    add_sub(ctx, a, b, true, out);
+  });
+}
+
+int th_rescale(th_ctx* ctx, const th_ct* ct, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    check_ct(ctx, ct);
+    const th_ct* cs[1] = {ct};
+    rescale_many(ctx, cs, 1, out);
+  });
+}
+
+int th_rescale_batch(th_ctx* ctx, const th_ct* const* cts, size_t count, th_ct** outs) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(outs && (cts || count == 0), "bad argument");
+    if (count) rescale_many(ctx, cts, count, outs);
+  });
+}
+
+int th_decrypt(th_ctx* ctx, const th_ct* ct, const th_sk* sk, double* out) {
+  return th_batch_decrypt(ctx, &ct, 1, sk, out);
+}
+
+int th_batch_decrypt(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, double* out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out || count == 0, "null output");
+    check_decrypt_args(ctx, cts, count, sk);
+    if (!count) return;
+    const size_t S = ctx->N / 2;
+    OpScope sc(ctx);
+    double* dev = (double*)sc.dev(count * S * 8);
+    queue_decrypt(sc, cts, count, sk, dev, nullptr, 0, 0);
+    download(ctx, out, dev, count * S * 8);
+  });
+}
+
+int th_batch_decrypt_segsum(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, uint32_t d,
+                            uint32_t cols, double* out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out || count == 0, "null output");
+    need(d >= 1 && cols >= 1 && (uint64_t)d * cols <= ctx->N / 2, "segments must fit in N/2 slots");
+    check_decrypt_args(ctx, cts, count, sk);
+    if (!count) return;
+    OpScope sc(ctx);
+    double* dev = (double*)sc.dev(count * cols * 8);
+    queue_decrypt(sc, cts, count, sk, nullptr, dev, d, cols);
+    download(ctx, out, dev, count * cols * 8);
+  });
+}
+
+int th_batch_decrypt_device(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, double* dev_out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(dev_out || count == 0, "null output");
+    check_decrypt_args(ctx, cts, count, sk);
+    if (!count) return;
+    OpScope sc(ctx);
+    queue_decrypt(sc, cts, count, sk, dev_out, nullptr, 0, 0);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int th_ct_free(th_ct* ct) {
+  return guarded([&] {
+    if (!ct) return;
+    ct->ctx->pool.put(ct->d);
+    delete ct;
+  });
+}
+
+int th_ct_info(const th_ct* ct, uint32_t* limbs, double* scale) {
+  return guarded([&] {
+    need(ct != nullptr, "null ciphertext");
+    if (limbs) *limbs = ct->limbs;
+    if (scale) *scale = ct->scale;
+  });
+}
+
+int th_ct_download(th_ctx* ctx, const th_ct* ct, uint64_t* c0, uint64_t* c1) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    check_ct(ctx, ct);
+    need(c0 && c1, "null output");
+    const size_t bytes = ct->limbs * poly_bytes(ctx);
+    download(ctx, c0, ct->d, bytes);
+    download(ctx, c1, ct->d + (size_t)ct->limbs * ctx->N, bytes);
+  });
+}
+
+int th_ct_upload(th_ctx* ctx, const uint64_t* c0, const uint64_t* c1, uint32_t limbs, double scale, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out && c0 && c1, "bad argument");
+    need(limbs >= 1 && limbs <= ctx->L, "limbs must be in [1, L]");
+    const size_t ln = (size_t)limbs * ctx->N;
+    for (uint32_t l = 0; l < limbs; ++l)
+      for (uint32_t i = 0; i < ctx->N; ++i)
+        need(c0[(size_t)l * ctx->N + i] < ctx->q[l] && c1[(size_t)l * ctx->N + i] < ctx->q[l],
+             "residues must be reduced modulo their limb prime");
+    th_ct* ct = new_ct(ctx, limbs, scale);
+    OpScope sc(ctx);
+    const uint64_t* u0 = (const uint64_t*)sc.upload(c0, ln * 8);
+    const uint64_t* u1 = (const uint64_t*)sc.upload(c1, ln * 8);
+    HIPCHK(hipMemcpyAsync(ct->d, u0, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    HIPCHK(hipMemcpyAsync(ct->d + ln, u1, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    *out = ct;
+  });
+}
+
+int th_ct_export(th_ctx* ctx, const th_ct* ct, uint8_t* buf, size_t cap, size_t* len) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    check_ct(ctx, ct);
+    need(len != nullptr, "null length");
+    const size_t pb = ct->limbs * poly_bytes(ctx);
+    *len = 8 + 2 * pb;  // serialize.rs:71-77
+    if (!buf) return;
+    need(cap >= *len, "buffer too small");
+    memcpy(buf, &ct->scale, 8);
+    download(ctx, buf + 8, ct->d, 2 * pb);
+  });
+}
+
+int th_ct_import(th_ctx* ctx, const uint8_t* buf, size_t len, uint32_t limbs, th_ct** out) {
+  return guarded([&] {
+    need(ctx && buf && out, "bad argument");
+    const size_t pb = (size_t)limbs * ctx->N * 8;
+    need(limbs >= 1 && limbs <= ctx->L, "limbs must be in [1, L]");
+    need(len == 8 + 2 * pb, "Expected " + std::to_string(8 + 2 * pb) + " bytes for Ciphertext, got " +
+                                std::to_string(len));  // serialize.rs:82-88
+    double scale;
+    memcpy(&scale, buf, 8);
+    std::vector<uint64_t> c0(pb / 8), c1(pb / 8);
+    memcpy(c0.data(), buf + 8, pb);
+    memcpy(c1.data(), buf + 8 + pb, pb);
+    int rc = th_ct_upload(ctx, c0.data(), c1.data(), limbs, scale, out);
+    if (rc != TH_OK) raise(rc, g_err);
+  });
+}
+
+int th_pk_export(th_ctx* ctx, const th_pk* pk, uint8_t* buf, size_t cap, size_t* len) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(pk && pk->ctx == ctx && len, "bad argument");
+    const size_t pb = ctx->L * poly_bytes(ctx);
+    *len = 2 * pb;  // serialize.rs:48-52
+    if (!buf) return;
+    need(cap >= *len, "buffer too small");
+    download(ctx, buf, pk->d, 2 * pb);
+  });
+}
+
+int th_pk_import(th_ctx* ctx, const uint8_t* buf, size_t len, th_pk** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(buf && out, "bad argument");
+    const size_t pb = ctx->L * poly_bytes(ctx);
+    need(len == 2 * pb, "Expected " + std::to_string(2 * pb) + " bytes for PublicKey, got " +
+                            std::to_string(len));  // serialize.rs:57-63
+    const uint64_t* w = (const uint64_t*)buf;
+    for (uint32_t l = 0; l < ctx->L; ++l)
+      for (uint32_t i = 0; i < ctx->N; ++i) {
+        uint64_t b, a;
+        memcpy(&b, buf + ((size_t)l * ctx->N + i) * 8, 8);
+        memcpy(&a, buf + pb + ((size_t)l * ctx->N + i) * 8, 8);
+        need(b < ctx->q[l] && a < ctx->q[l], "residues must be reduced modulo their limb prime");
+      }
+    (void)w;
+    th_pk* pk = new th_pk{ctx, (uint64_t*)ctx->pool.get(2 * pb)};
+    OpScope sc(ctx);
+    const void* up = sc.upload(buf, 2 * pb);
+    HIPCHK(hipMemcpyAsync(pk->d, up, 2 * pb, hipMemcpyDeviceToDevice, ctx->stream));
+    *out = pk;
+  });
+}
+
+int th_ntt_forward_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(polys || count == 0, "null polynomials");
+    ntt_batch(ctx, polys, count, limbs, on_device, false);
+  });
+}
+
+int th_ntt_inverse_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(polys || count == 0, "null polynomials");
+    ntt_batch(ctx, polys, count, limbs, on_device, true);
+  });
+}
+
+int th_dev_alloc(th_ctx* ctx, size_t bytes, void** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    *out = ctx->pool.get(bytes);
+  });
+}
+
+int th_dev_free(th_ctx* ctx, void* p) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(ctx->pool.owns(p), "pointer was not allocated by th_dev_alloc");
+    ctx->pool.put(p);
+  });
+}
+
+int th_memcpy_h2d(th_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int th_memcpy_d2h(th_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int th_ntt_time(th_ctx* ctx, uint64_t* dev_polys, size_t count, uint32_t limbs, int inverse, int reps, float* avg_ms) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(dev_polys && avg_ms && reps > 0 && count > 0, "bad argument");
+    need(limbs >= 1 && limbs <= ctx->L, "limbs must be in [1, L]");
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    try {
+      HIPCHK(hipEventRecord(e0, ctx->stream));
+      for (int r = 0; r < reps; ++r)
+        ntt_strided(ctx, inverse != 0, dev_polys, dev_polys, (uint32_t)(count * limbs), limbs);
+      HIPCHK(hipEventRecord(e1, ctx->stream));
+      HIPCHK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+      *avg_ms = ms / reps;
+    } catch (...) {
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+      throw;
+    }
+    HIPCHK(hipEventDestroy(e0));
+    HIPCHK(hipEventDestroy(e1));
+  });
+}
+
+}  // extern "C"

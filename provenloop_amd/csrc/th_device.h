@@ -1,0 +1,105 @@
+// Device-side definitions shared by the HIP kernels of the CKKS engine.
+//
+// Residues live in HBM as canonical u64 values in [0, q), limb-major:
+// a limb-polynomial is N consecutive u64, a ciphertext is [c0 | c1] with each
+// component L limb-polynomials back to back (the reference's RnsPoly layout,
+// tensafe-he-core/src/rns.rs:199-206, made contiguous).
+//
+// Two exact modular-multiply paths are used, chosen per prime:
+//  * "int":  64-bit Shoup multiply with a precomputed floor(w*2^64/q) and
+//            Harvey lazy reduction (values kept in [0, 4q)); any q < 2^62.
+//  * "fp64": for q < 2^41 the product w*x is split exactly into hi + lo with
+//            one FMA and the quotient comes from x*(w/q) rounded to nearest;
+//            the remainder is exact (all intermediate integers < 2^53). Six
+//            full-rate FP64 instructions per multiply.
+// Both produce the unique canonical residue, so results are bit-identical to
+// the reference's u128 Barrett multiply (tensafe-he-core/src/rns.rs:45-95).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace th {
+
+// Largest prime that takes the fp64 multiply path.
+constexpr uint64_t FP64_PRIME_LIMIT = 1ULL << 41;
+
+struct ShoupTw {
+  uint64_t w, ws;  // twiddle and floor(w * 2^64 / q)
+};
+struct Fp64Tw {
+  double w, wq;  // twiddle and w / q (correctly rounded)
+};
+
+// Per-limb constants; one array per context in device memory.
+struct LimbConst {
+  uint64_t q, two_q;
+  uint64_t n_inv, n_inv_s;    // N^{-1} and its Shoup companion
+  uint64_t last_w, last_ws;   // inv_tw[1] * N^{-1}: last inverse stage with the scaling folded in
+  double qd, qinv;            // q and 1/q as doubles (fp64 path)
+  double n_inv_d, n_inv_dq;
+  double last_wd, last_wdq;
+  const void* fwd;            // N twiddle pairs (ShoupTw or Fp64Tw), fwd[brv(i)] = psi^i
+  const void* inv;            // N twiddle pairs, inv[brv(i)] = psi^-i
+  uint32_t fp64;              // 1 if this limb uses the fp64 path
+  uint32_t pad_;
+};
+
+// ---------------------------------------------------------------- int path
+__device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t ws, uint64_t q) {
+  // x * w mod q in [0, 2q) for any x < 2^64 (w < q).
+  uint64_t qh = __umul64hi(x, ws);
+  return x * w - qh * q;
+}
+
+__device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t m) { return x >= m ? x - m : x; }
+
+// Exact a*b mod q for a, b < q < 2^63 (operands without a precomputed
+// companion): 128-bit product, quotient from the high word scaled by a
+// per-prime reciprocal, then at most two corrections.
+struct BarrettConst {
+  uint64_t q;
+  uint64_t r_hi, r_lo;  // floor((2^128 - 1) / q) as two words
+};
+
+__device__ __forceinline__ uint64_t mulmod_barrett(uint64_t a, uint64_t b, const BarrettConst& m) {
+  uint64_t lo = a * b;
+  uint64_t hi = __umul64hi(a, b);
+  // quotient estimate = floor((hi*2^64 + lo) * (r_hi*2^64 + r_lo) / 2^128), lo*r_lo term dropped
+  uint64_t t1_lo = lo * m.r_hi, t1_hi = __umul64hi(lo, m.r_hi);
+  uint64_t t2_lo = hi * m.r_lo, t2_hi = __umul64hi(hi, m.r_lo);
+  uint64_t mid = t1_lo + t2_lo;
+  uint64_t carry = mid < t1_lo ? 1 : 0;
+  uint64_t quot = hi * m.r_hi + t1_hi + t2_hi + carry;
+  uint64_t r = lo - quot * m.q;
+  r = csub(r, m.q);
+  r = csub(r, m.q);
+  return r;
+}
+
+// ---------------------------------------------------------------- fp64 path
+// x*w mod q as an exact integer in about (-q/2, q/2); requires |x| < 2^46, w < q < 2^41.
+__device__ __forceinline__ double mulmod_f64(double x, double w, double wq, double q) {
+  double hi = x * w;
+  double lo = __fma_rn(x, w, -hi);
+  double quot = __builtin_rint(x * wq);
+  double r = __fma_rn(-quot, q, hi);
+  return r + lo;
+}
+
+// x mod q into [0, q) for an exact integer |x| < 2^50.
+__device__ __forceinline__ double reduce_f64(double x, double q, double qinv) {
+  double quot = __builtin_rint(x * qinv);
+  double r = __fma_rn(-quot, q, x);
+  return r < 0.0 ? r + q : r;
+}
+
+// x mod q into about (-q/2, q/2) (no sign fix) for an exact integer |x| < 2^50.
+__device__ __forceinline__ double reduce_f64_signed(double x, double q, double qinv) {
+  double quot = __builtin_rint(x * qinv);
+  return __fma_rn(-quot, q, x);
+}
+
+__device__ __forceinline__ double u64_to_f64(uint64_t x) { return (double)x; }  // exact for x < 2^53
+__device__ __forceinline__ uint64_t f64_to_u64(double x) { return (uint64_t)x; }  // x integral, 0 <= x < 2^53
+
+}  // namespace th
