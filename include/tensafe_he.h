@@ -74,6 +74,19 @@ int th_ctx_sync(th_ctx* ctx);
 /* The context's HIP stream (hipStream_t), for callers that order their own work after it. */
 int th_ctx_stream(th_ctx* ctx, void** stream);
 
+/* Context options (no counterpart in the reference; defaults shown first).
+ * TH_OPT_SAMPLER: where seeded encrypt_pk draws (u, e0, e1):
+ *   TH_SAMPLER_DEVICE (default) - ChaCha20 + Box-Muller on the GPU, same
+ *     stream positions as the reference; the Gaussian uses the device's
+ *     log/cos, so a sample could differ from glibc's only if the two straddle
+ *     a rounding boundary (never observed; see the sampler tests);
+ *   TH_SAMPLER_HOST - the host draws them exactly as the reference does.
+ * TH_OPT_FORCE_SERIAL_SAMPLER: 1 makes the device sampler replay every
+ *   stream serially (the path taken after a range_u32 rejection); testing only. */
+enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2 };
+enum { TH_SAMPLER_DEVICE = 0, TH_SAMPLER_HOST = 1 };
+int th_ctx_set_option(th_ctx* ctx, int option, int64_t value);
+
 /* ---------------------------------------------------------------- keys */
 /* Replaces CkksContext.keygen (lib.rs:91-99, ciphertext.rs:77-103). */
 int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out);

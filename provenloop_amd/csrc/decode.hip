@@ -16,13 +16,10 @@
 // independent parts of N/2^p values (one workgroup each, in LDS); the last p
 // stages combine the parts element-wise in a second kernel, which also forms
 // the ZeRo-MOAI segment sums.
+#include "fft_device.h"
 #include "poly_kernels.h"
 
 namespace th {
-
-__device__ __forceinline__ uint32_t brv_bits(uint32_t x, uint32_t bits) {
-  return bits ? (__brev(x) >> (32 - bits)) : 0;
-}
 
 // Rust `u128 as f64`: round to nearest, ties to even.
 __device__ __forceinline__ double u128_to_f64(uint64_t hi, uint64_t lo) {
@@ -96,44 +93,12 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_parts(const DecodeJob* _
     im[pos] = -c * twist_im[j];
   }
   __syncthreads();
-  for (uint32_t s = 0; s < lb; ++s) {
-    const uint32_t half = 1u << s;
-    const double* wr = stage_re + (half - 1);
-    const double* wi = stage_im + (half - 1);
-    for (uint32_t b = threadIdx.x; b < M / 2; b += blockDim.x) {
-      const uint32_t k = b & (half - 1);
-      const uint32_t i0 = ((b >> s) << (s + 1)) | k;
-      const uint32_t i1 = i0 + half;
-      const double w_re = wr[k], w_im = wi[k];
-      const double x_re = re[i1], x_im = im[i1];
-      const double v_re = w_re * x_re - w_im * x_im;
-      const double v_im = w_re * x_im + w_im * x_re;
-      const double u_re = re[i0], u_im = im[i0];
-      re[i0] = u_re + v_re;
-      im[i0] = u_im + v_im;
-      re[i1] = u_re - v_re;
-      im[i1] = u_im - v_im;
-    }
-    __syncthreads();
-  }
+  dit_stages_lds(re, im, lb, stage_re, stage_im);
   double* out = jb.parts + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[i];
     out[M + i] = im[i];
   }
-}
-
-// complex multiply-accumulate in the reference's order: returns (u + w*x, u - w*x)
-struct Cx {
-  double re, im;
-};
-__device__ __forceinline__ void dit(Cx u, Cx x, double w_re, double w_im, Cx& top, Cx& bot) {
-  const double v_re = w_re * x.re - w_im * x.im;
-  const double v_im = w_re * x.im + w_im * x.re;
-  top.re = u.re + v_re;
-  top.im = u.im + v_im;
-  bot.re = u.re - v_re;
-  bot.im = u.im - v_im;
 }
 
 template <int LP>
@@ -192,13 +157,11 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* _
 
 size_t decode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 
-static uint32_t parts_log(uint32_t logn) { return logn <= 13 ? 0 : logn - 13; }
-
 hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t d, uint32_t cols, hipStream_t s) {
   if (!njobs) return hipSuccess;
-  const uint32_t lp = parts_log(logn);
+  const uint32_t lp = fft_parts_log(logn);
   const uint32_t M = (1u << logn) >> lp;
   const size_t lds_a = (size_t)2 * M * sizeof(double);
   const size_t lds_b = (size_t)(1u << logn) / 2 * sizeof(double);

@@ -1,0 +1,34 @@
+// Job descriptors and launchers of the GPU encoder and randomness sampler.
+#pragma once
+#include "th_internal.h"
+
+namespace th {
+
+struct EncodeJob {
+  const double* z;     // N/2 padded slots
+  const uint8_t* u;    // sample_ternary values {0,1,2}, or null
+  const int64_t* e0;   // rounded Gaussian e0, or null (plain encode)
+  const int64_t* e1;   // rounded Gaussian e1, or null
+  uint64_t* dst;       // [M (L) | E1 (L) | U (L)] limb-polys; only M when e1/u are null
+  double* parts;       // scratch, encode_parts_doubles(logn) doubles
+};
+
+// Encode z and write the per-limb residues of m (+ e0), e1 and u.
+hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
+                         const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
+                         uint32_t L, hipStream_t s);
+size_t encode_parts_doubles(uint32_t logn);
+
+struct SampleJob {
+  uint64_t seed;  // TenSafeRng::from_seed(seed)
+  uint8_t* u;     // n ternary values
+  int64_t* e0;    // n rounded Gaussians
+  int64_t* e1;    // n rounded Gaussians
+};
+
+// encrypt_pk's randomness (ciphertext.rs:255-273) for each job, drawn from the
+// job's ChaCha20 stream in the reference's order. force_serial makes every job
+// take the serial path that handles range_u32 rejections (for testing).
+hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s);
+
+}  // namespace th

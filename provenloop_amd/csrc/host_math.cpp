@@ -206,61 +206,6 @@ void Encoder::init(uint32_t nn) {
       sincos(angle, &stage_im[half - 1 + k], &stage_re[half - 1 + k]);
     }
   }
-  brv.resize(n);
-  for (uint32_t i = 0; i < n; ++i) {
-    uint32_t r = 0, v = i;
-    for (uint32_t b = 0; b < logn; ++b) {
-      r = (r << 1) | (v & 1);
-      v >>= 1;
-    }
-    brv[i] = r;
-  }
-}
-
-void Encoder::fft(double* re, double* im) const {
-  for (uint32_t i = 0; i < n; ++i) {
-    uint32_t j = brv[i];
-    if (i < j) {
-      double t = re[i]; re[i] = re[j]; re[j] = t;
-      t = im[i]; im[i] = im[j]; im[j] = t;
-    }
-  }
-  for (uint32_t s = 0; s < logn; ++s) {
-    const uint32_t half = 1u << s;
-    const double* wr = &stage_re[half - 1];
-    const double* wi = &stage_im[half - 1];
-    for (uint32_t g = 0; g < n; g += 2 * half) {
-      for (uint32_t k = 0; k < half; ++k) {
-        const uint32_t a = g + k, b = a + half;
-        const double vr = wr[k] * re[b] - wi[k] * im[b];
-        const double vi = wr[k] * im[b] + wi[k] * re[b];
-        const double ur = re[a], ui = im[a];
-        re[a] = ur + vr;
-        im[a] = ui + vi;
-        re[b] = ur - vr;
-        im[b] = ui - vi;
-      }
-    }
-  }
-}
-
-void Encoder::encode_i64(const double* z, size_t len, int64_t* out) const {
-  // encoding.rs:173-207 and :250-278
-  const uint32_t slots = n / 2;
-  std::vector<double> re(n, 0.0), im(n, 0.0);
-  for (uint32_t k = 0; k < slots; ++k) {
-    double v = k < len ? z[k] : 0.0;
-    re[k] = v;
-    re[n - 1 - k] = v;
-  }
-  fft(re.data(), im.data());
-  const double inv_n = 1.0 / (double)n;
-  for (uint32_t j = 0; j < n; ++j) {
-    double a_re = re[j] * inv_n;
-    double a_im = im[j] * inv_n;
-    double c = a_re * twist_re[j] + a_im * twist_im[j];
-    out[j] = round_sat(c * 1099511627776.0);
-  }
 }
 
 }  // namespace th

@@ -1,9 +1,9 @@
 // Host-side arithmetic of the engine: parameter tables, the seeded ChaCha20
-// stream and samplers, and the f64 canonical-embedding encoder.
+// stream and samplers (key generation, secret-key encryption, the host
+// sampler option) and the f64 FFT tables of the encoder.
 //
 // These follow the reference's definitions exactly (they decide ciphertext
-// bits), but are this library's own implementation: the stream is produced in
-// whole 64-byte blocks into a buffer and the encoder runs on flat arrays.
+// bits), but are this library's own implementation.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -50,16 +50,13 @@ void draw_ternary(ChaChaStream& s, size_t n, uint8_t* out);
 // round(gaussian) as i64, half away from zero, saturating (sampling.rs:51-58).
 void draw_gaussian(ChaChaStream& s, size_t n, int64_t* out);
 
-// f64 encoder tables and transforms (tensafe-he-core/src/encoding.rs:24-278).
+// f64 tables of the canonical-embedding FFT (tensafe-he-core/src/encoding.rs:39-80),
+// uploaded once per context for the GPU encoder and decoder.
 struct Encoder {
   uint32_t n = 0, logn = 0;
   std::vector<double> twist_re, twist_im;   // cos/sin(pi j / N)
   std::vector<double> stage_re, stage_im;   // per-stage DIT twiddles, stage s at offset 2^s - 1
-  std::vector<uint32_t> brv;
   void init(uint32_t n);
-  void fft(double* re, double* im) const;
-  // z (len <= N/2) -> round(coeff * 2^40) as i64 per coefficient.
-  void encode_i64(const double* z, size_t len, int64_t* out) const;
 };
 
 }  // namespace th

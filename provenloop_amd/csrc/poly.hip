@@ -43,27 +43,6 @@ __global__ void k_ct_addsub(const AddJob* __restrict__ jobs, const uint64_t* __r
   }
 }
 
-// encrypt_pk inputs before the forward NTT (ciphertext.rs:250-296):
-//   M_l = (m + e0) mod q_l, U_l = u mod q_l, E1_l = e1 mod q_l.
-// Layout of dst per job: [M (L) | E1 (L) | U (L)] limb-polynomials.
-__global__ void k_encrypt_prep(const EncPrepJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
-                               uint32_t n, uint32_t L) {
-  const EncPrepJob jb = jobs[blockIdx.y];
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    const int64_t m = jb.m[i], e0 = jb.e0[i];
-    const int64_t e1 = jb.e1 ? jb.e1[i] : 0;
-    const uint8_t u = jb.u ? jb.u[i] : 1;
-    for (uint32_t l = 0; l < L; ++l) {
-      const BarrettConst c = bc[l];
-      const uint64_t ql = c.q;
-      jb.dst[(uint64_t)l * n + i] = addmod(signed_residue(m, c), signed_residue(e0, c), ql);
-      if (jb.e1) jb.dst[(uint64_t)(L + l) * n + i] = signed_residue(e1, c);
-      // ciphertext.rs:261-266: 0 -> q-1, 1 -> 0, 2 -> 1
-      if (jb.u) jb.dst[(uint64_t)(2 * L + l) * n + i] = u == 0 ? ql - 1 : (u == 1 ? 0 : 1);
-    }
-  }
-}
-
 // dst[l][i] = x[i] mod q_l for signed integer coefficients (encoding.rs:193-204).
 __global__ void k_signed_to_rns(const int64_t* __restrict__ x, uint64_t* __restrict__ dst,
                                 const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L) {
@@ -152,13 +131,6 @@ hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_lim
                             uint32_t n, hipStream_t s) {
   if (!njobs) return hipSuccess;
   hipLaunchKernelGGL(k_ct_addsub, grid_for(2 * max_limbs * n, njobs), dim3(256), 0, s, jobs, q, n);
-  return hipGetLastError();
-}
-
-hipError_t launch_encrypt_prep(const EncPrepJob* jobs, uint32_t njobs, const BarrettConst* bc, uint32_t n,
-                               uint32_t L, hipStream_t s) {
-  if (!njobs) return hipSuccess;
-  hipLaunchKernelGGL(k_encrypt_prep, grid_for(n, njobs), dim3(256), 0, s, jobs, bc, n, L);
   return hipGetLastError();
 }
 

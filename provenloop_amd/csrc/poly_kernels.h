@@ -21,14 +21,6 @@ struct AddJob {
   uint32_t sub;
 };
 
-struct EncPrepJob {
-  const int64_t* m;   // round(coeff * 2^40) per coefficient
-  const int64_t* e0;
-  const int64_t* e1;  // may be null (secret-key encryption)
-  const uint8_t* u;   // sample_ternary values {0,1,2}; may be null
-  uint64_t* dst;      // [M | E1 | U], L limb-polys each
-};
-
 struct EncCombineJob {
   const uint64_t* prep;  // NTT of [M | E1 | U]
   const uint64_t* pk_b;
@@ -75,8 +67,6 @@ hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_li
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
                             uint32_t n, hipStream_t s);
-hipError_t launch_encrypt_prep(const EncPrepJob* jobs, uint32_t njobs, const BarrettConst* bc, uint32_t n,
-                               uint32_t L, hipStream_t s);
 hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
                                   uint32_t n, uint32_t L, hipStream_t s);
 hipError_t launch_rescale_combine(const RescaleJob* jobs, uint32_t njobs, const RescaleConst* rc, uint32_t n,

@@ -20,6 +20,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "encode_sample.h"
 #include "host_math.h"
 #include "poly_kernels.h"
 #include "tensafe_he.h"
@@ -164,6 +165,8 @@ struct th_ctx {
   double *d_twist_re = nullptr, *d_twist_im = nullptr, *d_stage_re = nullptr, *d_stage_im = nullptr;
   void* d_tables = nullptr;  // twiddle storage
   Encoder enc;
+  int host_sampler = 0;   // TH_OPT_SAMPLER
+  int force_serial = 0;   // TH_OPT_FORCE_SERIAL_SAMPLER
   DevicePool pool;
   StagingRing ring;
   std::mutex mu;
@@ -410,12 +413,12 @@ void destroy_ctx(th_ctx* c) {
 }
 
 // ---------------------------------------------------------------- host-side inputs
-void pad_input(const th_ctx* c, const double* z, size_t n, std::vector<double>& out) {
+void pad_input(const th_ctx* c, const double* z, size_t n, double* out) {
   // lib.rs:123-126: pad or truncate to N/2 slots
   const size_t S = c->N / 2;
-  out.assign(S, 0.0);
   const size_t m = std::min(n, S);
-  if (m) memcpy(out.data(), z, m * 8);
+  if (m) memcpy(out, z, m * 8);
+  if (m < S) memset(out + m, 0, (S - m) * 8);
 }
 
 // Upload signed coefficients and reduce them into L limb-polys at dst.
@@ -425,26 +428,52 @@ void upload_signed(OpScope& sc, const std::vector<int64_t>& x, uint64_t* dst, ui
   HIPCHK(launch_signed_to_rns(d, dst, c->d_bc, c->N, limbs, c->stream));
 }
 
-// encrypt_pk for `count` inputs with host-drawn or caller-supplied randomness.
-struct PkInput {
-  std::vector<int64_t> m, e0, e1;
-  std::vector<uint8_t> u;
-};
-
-void encrypt_pk_inputs(th_ctx* c, const th_pk* pk, std::vector<PkInput>& in, th_ct** outs) {
-  const uint32_t N = c->N, L = c->L;
-  const size_t count = in.size();
-  OpScope sc(c);
-  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
-  std::vector<EncPrepJob> pj(count);
+// GPU encode of `count` padded inputs (device, count x N/2) into dst + i*dst_stride:
+// M = m (+ e0), and E1, U when those are given (encoding.rs:173-207).
+void queue_encode(OpScope& sc, const double* z, size_t count, const uint8_t* u, const int64_t* e0,
+                  const int64_t* e1, uint64_t* dst, size_t dst_stride) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, S = N / 2;
+  double* parts = (double*)sc.dev(count * encode_parts_doubles(c->logn) * 8);
+  std::vector<EncodeJob> ej(count);
   for (size_t i = 0; i < count; ++i) {
-    pj[i].m = sc.up(in[i].m);
-    pj[i].e0 = sc.up(in[i].e0);
-    pj[i].e1 = sc.up(in[i].e1);
-    pj[i].u = sc.up(in[i].u);
-    pj[i].dst = prep + i * 3 * L * N;
+    ej[i].z = z + i * S;
+    ej[i].u = u ? u + i * N : nullptr;
+    ej[i].e0 = e0 ? e0 + i * N : nullptr;
+    ej[i].e1 = e1 ? e1 + i * N : nullptr;
+    ej[i].dst = dst + i * dst_stride;
+    ej[i].parts = parts + i * encode_parts_doubles(c->logn);
   }
-  HIPCHK(launch_encrypt_prep(sc.up(pj), (uint32_t)count, c->d_bc, N, L, c->stream));
+  HIPCHK(launch_encode(sc.up(ej), (uint32_t)count, c->d_bc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
+                       c->d_stage_im, c->logn, c->L, c->stream));
+}
+
+// encrypt_pk of `count` padded inputs zh (host, count x N/2). Randomness comes
+// from the device sampler (seeds), or from host arrays u/e0/e1 (count x N each).
+void encrypt_pk_many(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint64_t* seeds,
+                     const uint8_t* hu, const int64_t* he0, const int64_t* he1, th_ct** outs) {
+  const uint32_t N = c->N, L = c->L, S = N / 2;
+  OpScope sc(c);
+  const double* z = (const double*)sc.upload(zh, count * S * 8);
+  const uint8_t* u;
+  const int64_t *e0, *e1;
+  if (hu) {
+    u = (const uint8_t*)sc.upload(hu, count * N);
+    e0 = (const int64_t*)sc.upload(he0, count * N * 8);
+    e1 = (const int64_t*)sc.upload(he1, count * N * 8);
+  } else {
+    uint8_t* du = (uint8_t*)sc.dev(count * N);
+    int64_t* de0 = (int64_t*)sc.dev(count * N * 8);
+    int64_t* de1 = (int64_t*)sc.dev(count * N * 8);
+    std::vector<SampleJob> sj(count);
+    for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], du + i * N, de0 + i * N, de1 + i * N};
+    HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
+    u = du;
+    e0 = de0;
+    e1 = de1;
+  }
+  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
+  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N);
   ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
   std::vector<EncCombineJob> cj(count);
   std::vector<th_ct*> made;
@@ -465,15 +494,26 @@ void encrypt_pk_inputs(th_ctx* c, const th_pk* pk, std::vector<PkInput>& in, th_
   for (size_t i = 0; i < count; ++i) outs[i] = made[i];
 }
 
-void draw_pk_randomness(uint64_t seed, int has_seed, uint32_t N, PkInput& x) {
+// encrypt_pk's draws on the host (ciphertext.rs:255-273): u, then e0, then e1.
+void draw_pk_randomness(uint64_t seed, int has_seed, uint32_t N, uint8_t* u, int64_t* e0, int64_t* e1) {
   ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
-  // ciphertext.rs:255-273: u, then e0, then e1
-  x.u.resize(N);
-  x.e0.resize(N);
-  x.e1.resize(N);
-  draw_ternary(s, N, x.u.data());
-  draw_gaussian(s, N, x.e0.data());
-  draw_gaussian(s, N, x.e1.data());
+  draw_ternary(s, N, u);
+  draw_gaussian(s, N, e0);
+  draw_gaussian(s, N, e1);
+}
+
+// Seeded encrypt_pk of `count` padded inputs through the configured sampler.
+void encrypt_pk_seeded(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint64_t* seeds,
+                       th_ct** outs) {
+  if (!c->host_sampler) {
+    encrypt_pk_many(c, pk, zh, count, seeds, nullptr, nullptr, nullptr, outs);
+    return;
+  }
+  const uint32_t N = c->N;
+  std::vector<uint8_t> u(count * N);
+  std::vector<int64_t> e0(count * N), e1(count * N);
+  parallel_for(count, [&](size_t i) { draw_pk_randomness(seeds[i], 1, N, &u[i * N], &e0[i * N], &e1[i * N]); });
+  encrypt_pk_many(c, pk, zh, count, nullptr, u.data(), e0.data(), e1.data(), outs);
 }
 
 // ---------------------------------------------------------------- decryption pipeline
@@ -566,14 +606,19 @@ void rescale_many(th_ctx* c, const th_ct* const* cts, size_t count, th_ct** outs
 }
 
 th_pt* encode_pt(th_ctx* c, const double* z, size_t n) {
-  std::vector<double> pad;
-  pad_input(c, z, n, pad);
-  std::vector<int64_t> m(c->N);
-  c->enc.encode_i64(pad.data(), pad.size(), m.data());
+  std::vector<double> pad(c->N / 2);
+  pad_input(c, z, n, pad.data());
   th_pt* pt = new th_pt{c, c->L, (uint64_t*)c->pool.get(c->L * poly_bytes(c))};
-  OpScope sc(c);
-  upload_signed(sc, m, pt->d, c->L);
-  ntt_strided(c, false, pt->d, pt->d, c->L, c->L);
+  try {
+    OpScope sc(c);
+    const double* zd = sc.up(pad);
+    queue_encode(sc, zd, 1, nullptr, nullptr, nullptr, pt->d, 0);
+    ntt_strided(c, false, pt->d, pt->d, c->L, c->L);
+  } catch (...) {
+    c->pool.put(pt->d);
+    delete pt;
+    throw;
+  }
   return pt;
 }
 
@@ -828,8 +873,6 @@ namespace {
 // (ciphertext.rs:167-229: encode, a for every limb, then e).
 th_ct* encrypt_sk_one(th_ctx* ctx, const th_sk* sk, const std::vector<double>& pad, ChaChaStream& s) {
   const uint32_t N = ctx->N, L = ctx->L;
-  std::vector<int64_t> m(N);
-  ctx->enc.encode_i64(pad.data(), pad.size(), m.data());
   std::vector<uint64_t> a((size_t)L * N);
   for (uint32_t l = 0; l < L; ++l)
     for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
@@ -841,8 +884,7 @@ th_ct* encrypt_sk_one(th_ctx* ctx, const th_sk* sk, const std::vector<double>& p
   try {
     OpScope sc(ctx);
     uint64_t* me = (uint64_t*)sc.dev(L * poly_bytes(ctx));
-    EncPrepJob pj{sc.up(m), sc.up(e), nullptr, nullptr, me};
-    HIPCHK(launch_encrypt_prep(sc.up(std::vector<EncPrepJob>{pj}), 1, ctx->d_bc, N, L, ctx->stream));
+    queue_encode(sc, sc.up(pad), 1, nullptr, sc.up(e), nullptr, me, 0);  // M = m + e
     const uint64_t* a_up = sc.up(a);
     HIPCHK(hipMemcpyAsync(c1, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
     ntt_strided(ctx, false, me, me, L, L);
@@ -864,8 +906,8 @@ int th_encrypt(th_ctx* ctx, const th_sk* sk, const double* z, size_t n, uint64_t
     TH_LOCK(ctx);
     need(out && sk && sk->ctx == ctx, "bad argument");
     need(z != nullptr || n == 0, "null input");
-    std::vector<double> pad;
-    pad_input(ctx, z, n, pad);
+    std::vector<double> pad(ctx->N / 2);
+    pad_input(ctx, z, n, pad.data());
     ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
     *out = encrypt_sk_one(ctx, sk, pad, s);
   });
@@ -880,8 +922,8 @@ int th_encrypt_batch(th_ctx* ctx, const th_sk* sk, const double* z, const uint64
     std::vector<th_ct*> made;
     try {
       for (size_t i = 0; i < count; ++i) {
-        std::vector<double> pad;
-        pad_input(ctx, z + i * stride, (size_t)lens[i], pad);
+        std::vector<double> pad(ctx->N / 2);
+        pad_input(ctx, z + i * stride, (size_t)lens[i], pad.data());
         made.push_back(encrypt_sk_one(ctx, sk, pad, s));
       }
     } catch (...) {
@@ -900,13 +942,17 @@ int th_encrypt_pk(th_ctx* ctx, const th_pk* pk, const double* z, size_t n, uint6
     TH_LOCK(ctx);
     need(out && pk && pk->ctx == ctx, "bad argument");
     need(z != nullptr || n == 0, "null input");
-    std::vector<PkInput> in(1);
-    std::vector<double> pad;
-    pad_input(ctx, z, n, pad);
-    in[0].m.resize(ctx->N);
-    ctx->enc.encode_i64(pad.data(), pad.size(), in[0].m.data());
-    draw_pk_randomness(seed, has_seed, ctx->N, in[0]);
-    encrypt_pk_inputs(ctx, pk, in, out);
+    std::vector<double> pad(ctx->N / 2);
+    pad_input(ctx, z, n, pad.data());
+    if (!has_seed) {  // OS entropy: draw the seed on the host like TenSafeRng::from_entropy
+      uint64_t s = 0;
+      FILE* f = fopen("/dev/urandom", "rb");
+      bool ok = f && fread(&s, 1, 8, f) == 8;
+      if (f) fclose(f);
+      if (!ok) s = (uint64_t)(uintptr_t)&s ^ 0xdeadbeefcafebabeULL;
+      seed = s;
+    }
+    encrypt_pk_seeded(ctx, pk, pad.data(), 1, &seed, out);
   });
 }
 
@@ -918,15 +964,9 @@ int th_encrypt_pk_explicit(th_ctx* ctx, const th_pk* pk, const double* z, size_t
     need(z != nullptr || n == 0, "null input");
     const uint32_t N = ctx->N;
     for (uint32_t i = 0; i < N; ++i) need(u[i] <= 2, "u values must be in {0, 1, 2}");
-    std::vector<PkInput> in(1);
-    std::vector<double> pad;
-    pad_input(ctx, z, n, pad);
-    in[0].m.resize(N);
-    ctx->enc.encode_i64(pad.data(), pad.size(), in[0].m.data());
-    in[0].u.assign(u, u + N);
-    in[0].e0.assign(e0, e0 + N);
-    in[0].e1.assign(e1, e1 + N);
-    encrypt_pk_inputs(ctx, pk, in, out);
+    std::vector<double> pad(N / 2);
+    pad_input(ctx, z, n, pad.data());
+    encrypt_pk_many(ctx, pk, pad.data(), 1, nullptr, u, e0, e1, out);
   });
 }
 
@@ -937,15 +977,27 @@ int th_encrypt_pk_batch(th_ctx* ctx, const th_pk* pk, const double* z, size_t n,
     need(outs && pk && pk->ctx == ctx && seeds, "bad argument");
     need(z != nullptr || count == 0, "null input");
     if (!count) return;
-    std::vector<PkInput> in(count);
-    parallel_for(count, [&](size_t i) {
-      std::vector<double> pad;
-      pad_input(ctx, z + i * stride, n, pad);
-      in[i].m.resize(ctx->N);
-      ctx->enc.encode_i64(pad.data(), pad.size(), in[i].m.data());
-      draw_pk_randomness(seeds[i], 1, ctx->N, in[i]);
-    });
-    encrypt_pk_inputs(ctx, pk, in, outs);
+    const size_t S = ctx->N / 2;
+    std::vector<double> pad(count * S);
+    for (size_t i = 0; i < count; ++i) pad_input(ctx, z + i * stride, n, pad.data() + i * S);
+    encrypt_pk_seeded(ctx, pk, pad.data(), count, seeds, outs);
+  });
+}
+
+int th_ctx_set_option(th_ctx* ctx, int option, int64_t value) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    switch (option) {
+      case TH_OPT_SAMPLER:
+        need(value == TH_SAMPLER_DEVICE || value == TH_SAMPLER_HOST, "unknown sampler");
+        ctx->host_sampler = value == TH_SAMPLER_HOST;
+        break;
+      case TH_OPT_FORCE_SERIAL_SAMPLER:
+        ctx->force_serial = value != 0;
+        break;
+      default:
+        raise(TH_EINVAL, "unknown option " + std::to_string(option));
+    }
   });
 }
 

@@ -418,6 +418,17 @@ class CkksContext:
     def sync(self):
         _lib.check(_lib.load().th_ctx_sync(self._h))
 
+    def set_sampler(self, where: str):
+        """Where seeded encrypt_pk draws its randomness: "device" (default) or "host"."""
+        value = {"device": _lib.TH_SAMPLER_DEVICE, "host": _lib.TH_SAMPLER_HOST}.get(where)
+        if value is None:
+            raise ValueError("sampler must be 'device' or 'host'")
+        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_SAMPLER, value))
+
+    def _force_serial_sampler(self, on: bool):
+        """Testing hook: replay every device stream serially (the rejection path)."""
+        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_FORCE_SERIAL_SAMPLER, int(on)))
+
     def _own(self, obj):
         if obj is None or not isinstance(obj, _Handle):
             raise TypeError("expected a tensafe_he key, plaintext or ciphertext object")

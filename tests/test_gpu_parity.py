@@ -119,6 +119,42 @@ def test_encrypt_pk_batch_matches_oracle(eng16, ref16, keys16):
         _ct_equal(eng16, ref16, cts[i], ref16.encrypt_pk(zs[i], rpk, 100 + i))
 
 
+@pytest.mark.parametrize("sampler", ["device", "host", "device-serial"])
+def test_samplers_match_oracle(eng16, ref16, keys16, sampler):
+    """Seeded encrypt_pk through each randomness path equals the oracle's, seed by seed."""
+    sk, pk, rsk, rpk = keys16
+    rng = np.random.default_rng(17)
+    eng16.set_sampler("host" if sampler == "host" else "device")
+    eng16._force_serial_sampler(sampler == "device-serial")
+    try:
+        seeds = [0, 1, 2**32 - 1, 2**32, 2**63 + 12345, 2**64 - 1] + [int(v) for v in rng.integers(0, 2**62, 6)]
+        if sampler == "device-serial":
+            seeds = seeds[:3]
+        zs = [rng.normal(size=8192) * 0.1 for _ in seeds]
+        cts = eng16.encrypt_pk_batch(zs, pk, seeds)
+        for ct, z, sd in zip(cts, zs, seeds):
+            _ct_equal(eng16, ref16, ct, ref16.encrypt_pk(z, rpk, sd))
+    finally:
+        eng16.set_sampler("device")
+        eng16._force_serial_sampler(False)
+
+
+def test_device_sampler_many_seeds(eng16, ref16, keys16):
+    """112 device-sampled encryptions (3.7M Gaussian draws) against the oracle."""
+    sk, pk, rsk, rpk = keys16
+    z = np.zeros(8192)
+    seeds = list(range(1000, 1112))
+    cts = eng16.encrypt_pk_batch([z] * len(seeds), pk, seeds)
+    for ct, sd in zip(cts, seeds):
+        _ct_equal(eng16, ref16, ct, ref16.encrypt_pk(z, rpk, sd))
+
+
+def test_encode_extremes_match_oracle(eng16, ref16):
+    for z in (np.zeros(8192), np.full(8192, 1e6), np.linspace(-3e3, 3e3, 8192), np.full(3, 5e12),
+              np.array([np.pi, -np.e, 1e-12, -1e-12])):
+        assert np.array_equal(eng16.pt_download(eng16.encode_to_ntt(z)), ref16.poly_data(ref16.encode_to_ntt(z)))
+
+
 def test_secret_key_encrypt_matches_oracle(eng16, ref16, keys16):
     sk, pk, rsk, rpk = keys16
     z = np.arange(10) * 0.5
