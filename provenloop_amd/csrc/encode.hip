@@ -32,7 +32,13 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   for (uint32_t jj = threadIdx.x; jj < M; jj += blockDim.x) {
     const uint32_t j = (jj << LP) | r;  // element at bit-reversed position part*M + pos
     const uint32_t pos = brv_bits(jj, lb);
-    re[pos] = j < S ? jb.z[j] : jb.z[n - 1 - j];
+    const uint32_t slot = j < S ? j : n - 1 - j;
+    double v;
+    if (jb.rep_d)  // inference_engine.py:1266-1269: [h | h | ... | 0]
+      v = slot < jb.rep_cols * jb.rep_d ? jb.z[slot % jb.rep_d] : 0.0;
+    else
+      v = jb.z[slot];
+    re[pos] = v;
     im[pos] = 0.0;
   }
   __syncthreads();

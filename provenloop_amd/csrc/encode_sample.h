@@ -5,7 +5,9 @@
 namespace th {
 
 struct EncodeJob {
-  const double* z;     // N/2 padded slots
+  const double* z;     // N/2 padded slots, or (rep_d > 0) one d-value vector
+  uint32_t rep_d;      // > 0: slots are rep_cols copies of z[0..rep_d) then zeros (ZeRo-MOAI replication)
+  uint32_t rep_cols;
   const uint8_t* u;    // sample_ternary values {0,1,2}, or null
   const int64_t* e0;   // rounded Gaussian e0, or null (plain encode)
   const int64_t* e1;   // rounded Gaussian e1, or null

@@ -431,13 +431,15 @@ void upload_signed(OpScope& sc, const std::vector<int64_t>& x, uint64_t* dst, ui
 // GPU encode of `count` padded inputs (device, count x N/2) into dst + i*dst_stride:
 // M = m (+ e0), and E1, U when those are given (encoding.rs:173-207).
 void queue_encode(OpScope& sc, const double* z, size_t count, const uint8_t* u, const int64_t* e0,
-                  const int64_t* e1, uint64_t* dst, size_t dst_stride) {
+                  const int64_t* e1, uint64_t* dst, size_t dst_stride, uint32_t rep_d = 0, uint32_t rep_cols = 0) {
   th_ctx* c = sc.c;
   const uint32_t N = c->N, S = N / 2;
   double* parts = (double*)sc.dev(count * encode_parts_doubles(c->logn) * 8);
   std::vector<EncodeJob> ej(count);
   for (size_t i = 0; i < count; ++i) {
-    ej[i].z = z + i * S;
+    ej[i].z = rep_d ? z + i * rep_d : z + i * S;
+    ej[i].rep_d = rep_d;
+    ej[i].rep_cols = rep_cols;
     ej[i].u = u ? u + i * N : nullptr;
     ej[i].e0 = e0 ? e0 + i * N : nullptr;
     ej[i].e1 = e1 ? e1 + i * N : nullptr;
@@ -450,6 +452,28 @@ void queue_encode(OpScope& sc, const double* z, size_t count, const uint8_t* u, 
 
 // encrypt_pk of `count` padded inputs zh (host, count x N/2). Randomness comes
 // from the device sampler (seeds), or from host arrays u/e0/e1 (count x N each).
+// Queue encrypt_pk of `count` inputs already on the device (z: count x N/2
+// padded slots, or count x rep_d values replicated rep_cols times) into the
+// ciphertext buffers out[i] (2 x L limb-polys each), drawing the randomness on
+// the device from seeds (host array).
+void queue_encrypt_pk(OpScope& sc, const th_pk* pk, const double* z, size_t count, const uint64_t* seeds,
+                      uint32_t rep_d, uint32_t rep_cols, uint64_t* const* out) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, L = c->L;
+  uint8_t* u = (uint8_t*)sc.dev(count * N);
+  int64_t* e0 = (int64_t*)sc.dev(count * N * 8);
+  int64_t* e1 = (int64_t*)sc.dev(count * N * 8);
+  std::vector<SampleJob> sj(count);
+  for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], u + i * N, e0 + i * N, e1 + i * N};
+  HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
+  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
+  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N, rep_d, rep_cols);
+  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
+  std::vector<EncCombineJob> cj(count);
+  for (size_t i = 0; i < count; ++i) cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, out[i]};
+  HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
+}
+
 void encrypt_pk_many(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint64_t* seeds,
                      const uint8_t* hu, const int64_t* he0, const int64_t* he1, th_ct** outs) {
   const uint32_t N = c->N, L = c->L, S = N / 2;
@@ -516,12 +540,26 @@ void encrypt_pk_seeded(th_ctx* c, const th_pk* pk, const double* zh, size_t coun
   encrypt_pk_many(c, pk, zh, count, nullptr, u.data(), e0.data(), e1.data(), outs);
 }
 
-// ---------------------------------------------------------------- decryption pipeline
-// Queue decrypt + decode of `count` ciphertexts; slots to out_dev (count x S) and/or
+// ---------------------------------------------------------------- pipelines on raw device ciphertexts
+// A ciphertext in device memory: c0 then c1, `limbs` limb-polys each.
+struct CtView {
+  const uint64_t* d;
+  uint32_t limbs;
+  double scale;
+};
+
+std::vector<CtView> views_of(const th_ct* const* cts, size_t count) {
+  std::vector<CtView> v(count);
+  for (size_t i = 0; i < count; ++i) v[i] = CtView{cts[i]->d, cts[i]->limbs, cts[i]->scale};
+  return v;
+}
+
+// Queue decrypt + decode of the views; slots to out_dev (count x S) and/or
 // segment sums to seg_dev (count x cols). Scratch lives in the caller's scope.
-void queue_decrypt(OpScope& sc, const th_ct* const* cts, size_t count, const th_sk* sk, double* out_dev,
-                   double* seg_dev, uint32_t d, uint32_t cols) {
+void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk, double* out_dev, double* seg_dev,
+                   uint32_t d, uint32_t cols) {
   th_ctx* c = sc.c;
+  const size_t count = cts.size();
   const uint32_t N = c->N, S = N / 2;
   uint64_t* dot = (uint64_t*)sc.dev(count * 2 * poly_bytes(c));
   double* parts = (double*)sc.dev(count * decode_parts_doubles(c->logn) * 8);
@@ -530,24 +568,61 @@ void queue_decrypt(OpScope& sc, const th_ct* const* cts, size_t count, const th_
   std::vector<DecodeJob> dec(count);
   uint32_t max_nl = 1;
   for (size_t i = 0; i < count; ++i) {
-    const th_ct* ct = cts[i];
+    const CtView& ct = cts[i];
     // ciphertext.rs:351: CRT branch iff scale > 1.5 * 2^40 and at least two limbs
-    const uint32_t nl = (ct->scale > kScale * 1.5 && ct->limbs >= 2) ? 2 : 1;
+    const uint32_t nl = (ct.scale > kScale * 1.5 && ct.limbs >= 2) ? 2 : 1;
     max_nl = std::max(max_nl, nl);
     uint64_t* o = dot + i * 2 * N;
-    dj[i] = DotJob{ct->d, ct->d + (size_t)ct->limbs * N, o, nl, 0};
+    dj[i] = DotJob{ct.d, ct.d + (size_t)ct.limbs * N, o, nl, 0};
     for (uint32_t l = 0; l < nl; ++l) nj.push_back(NttJob{o + (size_t)l * N, o + (size_t)l * N, l, 0});
     dec[i].m = o;
     dec[i].parts = parts + i * decode_parts_doubles(c->logn);
     dec[i].out = out_dev ? out_dev + i * S : nullptr;
     dec[i].seg = seg_dev ? seg_dev + i * cols : nullptr;
-    dec[i].scale = ct->scale;
+    dec[i].scale = ct.scale;
     dec[i].crt = nl == 2;
   }
   HIPCHK(launch_decrypt_dot(sc.up(dj), (uint32_t)count, c->d_bc, sk->d, N, max_nl, c->stream));
   ntt_list(sc, true, nj);
   HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
                        c->d_stage_im, c->logn, d, cols, c->stream));
+}
+
+// out[i] = in[i] x pt[i] on in[i]'s limbs (ciphertext.rs:422-429); out[i] has 2 x limbs limb-polys.
+void queue_ct_pt(OpScope& sc, const std::vector<CtView>& in, const uint64_t* const* pts, uint64_t* const* out) {
+  th_ctx* c = sc.c;
+  std::vector<CtPtJob> jobs(in.size());
+  uint32_t maxl = 1;
+  for (size_t i = 0; i < in.size(); ++i) {
+    const size_t ln = (size_t)in[i].limbs * c->N;
+    jobs[i] = CtPtJob{in[i].d, in[i].d + ln, pts[i], out[i], in[i].limbs, 0};
+    maxl = std::max(maxl, in[i].limbs);
+  }
+  HIPCHK(launch_ct_pt_mul(sc.up(jobs), (uint32_t)in.size(), maxl, c->d_bc, c->N, c->stream));
+}
+
+// Rescale (ciphertext.rs:476-535) of views that all have L >= 2 limbs into
+// out[i] (2 x (L-1) limb-polys each).
+void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* out) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N;
+  const size_t count = in.size();
+  const uint32_t L = in[0].limbs;
+  uint64_t* coef = (uint64_t*)sc.dev(count * 2 * L * poly_bytes(c));
+  std::vector<NttJob> inv;
+  inv.reserve(count * 2 * L);
+  for (size_t i = 0; i < count; ++i)
+    for (uint32_t k = 0; k < 2 * L; ++k)
+      inv.push_back(NttJob{in[i].d + (size_t)k * N, coef + (i * 2 * L + k) * N, k % L, 0});
+  ntt_list(sc, true, inv);
+  std::vector<RescaleJob> rj(count);
+  for (size_t i = 0; i < count; ++i) rj[i] = RescaleJob{coef + i * 2 * L * N, out[i]};
+  HIPCHK(launch_rescale_combine(sc.up(rj), (uint32_t)count, c->d_rc + (size_t)L * c->L, N, L, c->stream));
+  std::vector<NttJob> fwd;
+  fwd.reserve(count * 2 * (L - 1));
+  for (size_t i = 0; i < count; ++i)
+    for (uint32_t k = 0; k < 2 * (L - 1); ++k) fwd.push_back(NttJob{out[i] + (size_t)k * N, out[i] + (size_t)k * N, k % (L - 1), 0});
+  ntt_list(sc, false, fwd);
 }
 
 void check_decrypt_args(th_ctx* c, const th_ct* const* cts, size_t count, const th_sk* sk) {
@@ -565,36 +640,21 @@ void download(th_ctx* c, void* dst, const void* src_dev, size_t bytes) {
 }
 
 void rescale_many(th_ctx* c, const th_ct* const* cts, size_t count, th_ct** outs) {
-  const uint32_t N = c->N;
   const uint32_t L = cts[0]->limbs;
   for (size_t i = 0; i < count; ++i) {
     check_ct(c, cts[i]);
     need(cts[i]->limbs == L, "rescale_batch: all ciphertexts must have the same limb count");
   }
   need(L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);  // ciphertext.rs:479
-  OpScope sc(c);
-  uint64_t* coef = (uint64_t*)sc.dev(count * 2 * L * poly_bytes(c));
-  std::vector<NttJob> inv;
-  inv.reserve(count * 2 * L);
   std::vector<th_ct*> made;
-  std::vector<RescaleJob> rj(count);
   try {
-    for (size_t i = 0; i < count; ++i)
-      for (uint32_t k = 0; k < 2 * L; ++k)
-        inv.push_back(NttJob{cts[i]->d + (size_t)k * N, coef + (i * 2 * L + k) * N, k % L, 0});
-    ntt_list(sc, true, inv);
+    std::vector<uint64_t*> dst(count);
     for (size_t i = 0; i < count; ++i) {
-      th_ct* o = new_ct(c, L - 1, cts[i]->scale / (double)c->q[L - 1]);  // ciphertext.rs:533
-      made.push_back(o);
-      rj[i] = RescaleJob{coef + i * 2 * L * N, o->d};
+      made.push_back(new_ct(c, L - 1, cts[i]->scale / (double)c->q[L - 1]));  // ciphertext.rs:533
+      dst[i] = made.back()->d;
     }
-    HIPCHK(launch_rescale_combine(sc.up(rj), (uint32_t)count, c->d_rc + (size_t)L * c->L, N, L, c->stream));
-    std::vector<NttJob> fwd;
-    fwd.reserve(count * 2 * (L - 1));
-    for (size_t i = 0; i < count; ++i)
-      for (uint32_t k = 0; k < 2 * (L - 1); ++k)
-        fwd.push_back(NttJob{made[i]->d + (size_t)k * N, made[i]->d + (size_t)k * N, k % (L - 1), 0});
-    ntt_list(sc, false, fwd);
+    OpScope sc(c);
+    queue_rescale(sc, views_of(cts, count), dst.data());
   } catch (...) {
     for (th_ct* o : made) {
       c->pool.put(o->d);
@@ -623,22 +683,20 @@ th_pt* encode_pt(th_ctx* c, const double* z, size_t n) {
 }
 
 void ct_pt_many(th_ctx* c, const th_ct* const* cts, const th_pt* const* pts, size_t count, th_ct** outs) {
-  std::vector<CtPtJob> jobs(count);
   std::vector<th_ct*> made;
-  uint32_t maxl = 1;
   try {
+    std::vector<const uint64_t*> p(count);
+    std::vector<uint64_t*> dst(count);
     for (size_t i = 0; i < count; ++i) {
       check_ct(c, cts[i]);
       need(pts[i] && pts[i]->ctx == c, "plaintext belongs to another context");
       need(pts[i]->limbs >= cts[i]->limbs, "plaintext has fewer limbs than the ciphertext");
-      th_ct* o = new_ct(c, cts[i]->limbs, cts[i]->scale * cts[i]->scale);  // ciphertext.rs:427
-      made.push_back(o);
-      const size_t ln = (size_t)cts[i]->limbs * c->N;
-      jobs[i] = CtPtJob{cts[i]->d, cts[i]->d + ln, pts[i]->d, o->d, cts[i]->limbs, 0};
-      maxl = std::max(maxl, cts[i]->limbs);
+      made.push_back(new_ct(c, cts[i]->limbs, cts[i]->scale * cts[i]->scale));  // ciphertext.rs:427
+      dst[i] = made.back()->d;
+      p[i] = pts[i]->d;
     }
     OpScope sc(c);
-    HIPCHK(launch_ct_pt_mul(sc.up(jobs), (uint32_t)count, maxl, c->d_bc, c->N, c->stream));
+    queue_ct_pt(sc, views_of(cts, count), p.data(), dst.data());
   } catch (...) {
     for (th_ct* o : made) {
       c->pool.put(o->d);
@@ -1112,7 +1170,7 @@ int th_batch_decrypt(th_ctx* ctx, const th_ct* const* cts, size_t count, const t
     const size_t S = ctx->N / 2;
     OpScope sc(ctx);
     double* dev = (double*)sc.dev(count * S * 8);
-    queue_decrypt(sc, cts, count, sk, dev, nullptr, 0, 0);
+    queue_decrypt(sc, views_of(cts, count), sk, dev, nullptr, 0, 0);
     download(ctx, out, dev, count * S * 8);
   });
 }
@@ -1127,7 +1185,7 @@ int th_batch_decrypt_segsum(th_ctx* ctx, const th_ct* const* cts, size_t count, 
     if (!count) return;
     OpScope sc(ctx);
     double* dev = (double*)sc.dev(count * cols * 8);
-    queue_decrypt(sc, cts, count, sk, nullptr, dev, d, cols);
+    queue_decrypt(sc, views_of(cts, count), sk, nullptr, dev, d, cols);
     download(ctx, out, dev, count * cols * 8);
   });
 }
@@ -1139,8 +1197,57 @@ int th_batch_decrypt_device(th_ctx* ctx, const th_ct* const* cts, size_t count, 
     check_decrypt_args(ctx, cts, count, sk);
     if (!count) return;
     OpScope sc(ctx);
-    queue_decrypt(sc, cts, count, sk, dev_out, nullptr, 0, 0);
+    queue_decrypt(sc, views_of(cts, count), sk, dev_out, nullptr, 0, 0);
     HIPCHK(hipStreamSynchronize(ctx->stream));
+  });
+}
+
+int th_lora_a_pass(th_ctx* ctx, const th_pk* pk, const th_sk* sk, const double* hidden, uint32_t n_inputs,
+                   uint32_t d, const uint64_t* seeds, const th_pt* const* pts, const uint32_t* pt_input,
+                   uint32_t n_pts, int do_rescale, double* out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(pk && pk->ctx == ctx && sk && sk->ctx == ctx, "keys belong to another context");
+    need(n_inputs > 0 && hidden && seeds && out, "bad argument");
+    need(n_pts == 0 || (pts && pt_input), "bad argument");
+    const uint32_t N = ctx->N, S = N / 2, L = ctx->L;
+    need(d >= 1 && d <= S, "d must be in [1, N/2]");
+    need(!do_rescale || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
+    const uint32_t cols = S / d;  // inference_engine.py:1258
+    for (uint32_t j = 0; j < n_pts; ++j) {
+      need(pt_input[j] < n_inputs, "pt_input index out of range");
+      need(pts[j] && pts[j]->ctx == ctx && pts[j]->limbs == L, "plaintext belongs to another context");
+    }
+    if (!n_pts) return;
+    const size_t ctb = 2 * L * poly_bytes(ctx);
+    OpScope sc(ctx);
+    const double* z = (const double*)sc.upload(hidden, (size_t)n_inputs * d * 8);
+    uint64_t* cts = (uint64_t*)sc.dev(n_inputs * ctb);
+    std::vector<uint64_t*> ct_ptr(n_inputs);
+    for (uint32_t i = 0; i < n_inputs; ++i) ct_ptr[i] = cts + (size_t)i * 2 * L * N;
+    queue_encrypt_pk(sc, pk, z, n_inputs, seeds, d, cols, ct_ptr.data());
+    // products ct[pt_input[j]] x pts[j] (inference_engine.py:1311)
+    uint64_t* prods = (uint64_t*)sc.dev(n_pts * ctb);
+    std::vector<CtView> in(n_pts), views(n_pts);
+    std::vector<const uint64_t*> p(n_pts);
+    std::vector<uint64_t*> dst(n_pts);
+    for (uint32_t j = 0; j < n_pts; ++j) {
+      in[j] = CtView{ct_ptr[pt_input[j]], L, kScale};
+      p[j] = pts[j]->d;
+      dst[j] = prods + (size_t)j * 2 * L * N;
+      views[j] = CtView{dst[j], L, kScale * kScale};
+    }
+    queue_ct_pt(sc, in, p.data(), dst.data());
+    if (do_rescale) {
+      uint64_t* res = (uint64_t*)sc.dev(n_pts * 2 * (L - 1) * poly_bytes(ctx));
+      std::vector<uint64_t*> rdst(n_pts);
+      for (uint32_t j = 0; j < n_pts; ++j) rdst[j] = res + (size_t)j * 2 * (L - 1) * N;
+      queue_rescale(sc, views, rdst.data());
+      for (uint32_t j = 0; j < n_pts; ++j) views[j] = CtView{rdst[j], L - 1, kScale * kScale / (double)ctx->q[L - 1]};
+    }
+    double* seg = (double*)sc.dev((size_t)n_pts * cols * 8);
+    queue_decrypt(sc, views, sk, nullptr, seg, d, cols);
+    download(ctx, out, seg, (size_t)n_pts * cols * 8);
   });
 }
 

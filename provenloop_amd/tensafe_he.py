@@ -342,6 +342,29 @@ class CkksContext:
                                                            len(cts), self._own(sk), d, cols, _lib.ptr(out)))
         return out
 
+    def lora_a_pass(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden: np.ndarray, seeds, pts,
+                    pt_input, rescale: bool = True) -> np.ndarray:
+        """Whole encrypted LoRA-A pass in one call (see th_lora_a_pass).
+
+        hidden: [n_inputs, d] float64; seeds: n_inputs encrypt_pk seeds; pts: cached
+        plaintext batches; pt_input[j]: the input that pts[j] multiplies. Returns the
+        [len(pts), (N/2)//d] segment sums of the decrypted products.
+        """
+        h = np.ascontiguousarray(hidden, dtype=np.float64)
+        if h.ndim != 2:
+            raise ValueError("hidden must be [n_inputs, d]")
+        n_in, d = h.shape
+        sd = np.ascontiguousarray(seeds, dtype=np.uint64)
+        pin = np.ascontiguousarray(pt_input, dtype=np.uint32)
+        if sd.size != n_in or pin.size != len(pts):
+            raise ValueError("need one seed per input and one input index per plaintext")
+        cols = self.num_slots // d
+        out = np.zeros((len(pts), cols), np.float64)
+        _lib.check(_lib.load().th_lora_a_pass(self._h, self._own(pk), self._own(sk), _lib.ptr(h), n_in, d,
+                                              _lib.ptr(sd), _lib.handle_array([self._own(p) for p in pts]),
+                                              _lib.ptr(pin), len(pts), int(rescale), _lib.ptr(out)))
+        return out
+
     def batch_decrypt_to_device(self, cts, sk: TenSafeSecretKey, dev_ptr: int):
         """Decrypt into device memory at dev_ptr (len(cts) x num_slots float64)."""
         cts = list(cts)

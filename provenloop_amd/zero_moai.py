@@ -85,27 +85,25 @@ def lora_deltas(ctx: CkksContext, pk: TenSafePublicKey, sk: TenSafeSecretKey, hi
 
     hidden[i] is input i (length d); adapters[i] lists the projections that
     read input i (e.g. q and v of one layer share the layer input). Returns
-    (deltas, intermediates): deltas[i][j] = B_ij @ (A_ij h_i) computed with
-    A_ij h_i under encryption, one host synchronisation for the whole set.
+    (deltas, intermediates): deltas[i][j] = B_ij @ (A_ij h_i) with A_ij h_i
+    computed under encryption. The whole set is one th_lora_a_pass call: one
+    encrypt_pk batch, one product launch, one rescale batch and one GPU
+    decrypt with a single device-to-host copy.
     """
-    S = ctx.num_slots
     d = adapters[0][0].d_model
+    S = ctx.num_slots
     cols = max(1, S // d)
-    reps = [replicate(h, S, d) for h in hidden]
-    cts = ctx.encrypt_pk_batch(reps, pk, list(seeds))
-    pairs_ct, pairs_pt, index = [], [], []
+    pts, pin, index = [], [], []
     for i, ads in enumerate(adapters):
         for j, ad in enumerate(ads):
             if ad.d_model != d:
                 raise ValueError("all adapters must share d_model")
             for b, pt in enumerate(ad.pts):
-                pairs_ct.append(cts[i])
-                pairs_pt.append(pt)
+                pts.append(pt)
+                pin.append(i)
                 index.append((i, j, b))
-    prods = ctx.ct_pt_mul_ntt_batch(pairs_ct, pairs_pt)
-    if rescale:
-        prods = ctx.rescale_batch(prods)
-    sums = ctx.batch_decrypt_segsum(prods, sk, d, cols)
+    H = np.stack([np.asarray(h, np.float64).ravel()[:d] for h in hidden])
+    sums = ctx.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale)
     inter: Dict = {}
     for row, (i, j, b) in enumerate(index):
         ad = adapters[i][j]

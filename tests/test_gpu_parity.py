@@ -288,6 +288,30 @@ def test_single_delta_config(eng16, ref16, keys16):
     assert np.linalg.norm(gpu - cpu) / np.linalg.norm(cpu) <= 1e-3
 
 
+def test_lora_a_pass_matches_composed_ops(eng16, ref16, keys16):
+    """th_lora_a_pass == encrypt_pk -> ct x pt -> (rescale) -> decrypt -> segment sums, both branches."""
+    sk, pk, rsk, rpk = keys16
+    rng = np.random.default_rng(33)
+    H = rng.normal(size=(3, 1536)) * 0.1
+    A = rng.normal(size=(16, 1536)) * 0.02
+    pts_f = [_packed_rows(A, b) for b in range(4)]
+    pts = [eng16.encode_to_ntt(p) for p in pts_f]
+    pin = [0, 0, 1, 2, 2, 2]
+    use = [0, 1, 2, 3, 0, 1]
+    seeds = [501, 502, 503]
+    for rescale in (True, False):
+        got = eng16.lora_a_pass(pk, sk, H, seeds, [pts[u] for u in use], pin, rescale=rescale)
+        assert got.shape == (6, 5)
+        rcts = [ref16.encrypt_pk(_packed_rows(np.tile(h, (5, 1)), 0), rpk, sd) for h, sd in zip(H, seeds)]
+        for row, (i, u) in enumerate(zip(pin, use)):
+            r = ref16.ct_pt_mul(rcts[i], pts_f[u])
+            if rescale:
+                r = ref16.rescale(r)
+            dec = ref16.decrypt(r, rsk)
+            exp = np.array([np.sum(dec[c * 1536:(c + 1) * 1536]) for c in range(5)])
+            assert np.max(np.abs(got[row] - exp)) <= 1e-9 * max(1.0, np.max(np.abs(exp)))
+
+
 # ------------------------------------------------------------------ wire format
 def test_serialization_matches_oracle_bytes(eng16, ref16, keys16, base_ct):
     sk, pk, rsk, rpk = keys16
