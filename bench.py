@@ -199,6 +199,63 @@ def cpu_model():
     return "unknown"
 
 
+def copy_calibration(ctx, nbytes, reps=3):
+    """A plain device-to-device copy of nbytes (the HIP runtime's blit kernel):
+    it reads and writes exactly nbytes of HBM, so its FETCH_SIZE / WRITE_SIZE
+    counters give the counter scale."""
+    from provenloop_amd import _lib
+
+    L = _lib.load()
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipDeviceSynchronize.argtypes = []
+    src, dst = C.c_void_p(), C.c_void_p()
+    _lib.check(L.th_dev_alloc(ctx._h, nbytes, C.byref(src)))
+    _lib.check(L.th_dev_alloc(ctx._h, nbytes, C.byref(dst)))
+    host = np.arange(nbytes // 8, dtype=np.uint64)
+    _lib.check(L.th_memcpy_h2d(ctx._h, src, _lib.ptr(host), nbytes))
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        if hip.hipMemcpy(dst, src, nbytes, 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy device-to-device failed")
+    if hip.hipDeviceSynchronize() != 0:
+        raise RuntimeError("hipDeviceSynchronize failed")
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    back = np.empty_like(host)
+    _lib.check(L.th_memcpy_d2h(ctx._h, _lib.ptr(back), dst, nbytes))
+    if not np.array_equal(back, host):
+        raise RuntimeError("calibration copy mismatch")
+    _lib.check(L.th_dev_free(ctx._h, src))
+    _lib.check(L.th_dev_free(ctx._h, dst))
+    return ms
+
+
+# The four largest primes q = 1 mod 2N (N = 16384) below 2^60 and below 2^40:
+# chains that exercise only the integer (60-bit) or only the FP64 (< 2^41)
+# butterfly path of the NTT.
+NTT_CHAINS = {
+    "default": None,
+    "int60": [1152921504606748673, 1152921504606683137, 1152921504606584833, 1152921504605962241],
+    "fp40": [1099510054913, 1099508121601, 1099507695617, 1099506515969],
+}
+
+
+def ntt_only(chain="default"):
+    from provenloop_amd import tensafe_he
+
+    q = NTT_CHAINS[chain]
+    ctx = tensafe_he.CkksContext(N) if q is None else tensafe_he.CkksContext(N, moduli=q)
+    ntt = ntt_roofline(ctx, reps=5)
+    copy_ms = copy_calibration(ctx, ntt["bytes_per_launch"] // 2)
+    print(json.dumps({
+        "metric": "batched NTT achieved GB/s (64 polys x 4 limbs, N=16384)",
+        "chain": chain, "moduli": ctx.moduli,
+        "ntt": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in ntt.items()},
+        "copy_calibration": {"bytes": ntt["bytes_per_launch"] // 2, "ms": round(copy_ms, 4)},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,11 +263,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ntt-only", action="store_true",
+                    help="only the batched-NTT launches plus a plain device copy of the same size "
+                         "(the copy calibrates HBM byte counters); prints one JSON line")
+    ap.add_argument("--ntt-chain", choices=sorted(NTT_CHAINS), default="default",
+                    help="modulus chain of the --ntt-only launches: the default 4-limb chain, or four "
+                         "60-bit (integer butterfly path) or four 40-bit (FP64 butterfly path) primes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by session/token "
               "with no cross-GPU exchange, so N GPUs scale the one-GPU figure)", file=sys.stderr)
         sys.exit(2)
+    if args.ntt_only:
+        ntt_only(args.ntt_chain)
+        return
 
     A, B = make_workload()
     ctx, sk, pk, adapters = gpu_setup(A, B)

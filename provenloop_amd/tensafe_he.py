@@ -180,6 +180,11 @@ class CkksContext:
     def num_limbs(self) -> int:
         return self._limbs
 
+    @property
+    def device(self) -> int:
+        """HIP device index the context's buffers and stream live on."""
+        return self._device
+
     def _new(self, cls, fn, *args):
         out = C.c_void_p()
         _lib.check(fn(*args, C.byref(out)))

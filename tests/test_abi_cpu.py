@@ -86,3 +86,12 @@ def test_product_never_imports_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
                 assert "liboracle" not in text, f
+
+
+def test_adapter_init_fails_loudly_without_gpu():
+    from provenloop_amd import adapter
+
+    if _lib.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(_lib.HipEngineError, match="no HIP device"):
+        adapter.init_tensafe_he(16384)
