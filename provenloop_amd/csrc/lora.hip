@@ -1,0 +1,31 @@
+// LoRA-B application on the device: delta_j = B_j @ intermediate_j
+// (demonstrator/server/inference_engine.py:1392), where intermediate_j is
+// gathered from the ZeRo-MOAI segment sums of projection j's plaintext
+// batches (:1379-1386): row r of the LoRA-A side is segment r % cols of
+// batch first_row + r / cols.
+#include "poly_kernels.h"
+
+namespace th {
+
+__global__ __launch_bounds__(256) void k_lora_b(const LoraBJob* __restrict__ jobs, const double* __restrict__ sums,
+                                                double* __restrict__ out, uint32_t cols) {
+  const LoraBJob jb = jobs[blockIdx.y];
+  const double* seg = sums + (size_t)jb.first_row * cols;  // batch-major: seg[b * cols + c]
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < jb.d_out; i += gridDim.x * blockDim.x) {
+    const double* brow = jb.b + (size_t)i * jb.rank;
+    double acc = 0.0;
+    for (uint32_t r = 0; r < jb.rank; ++r) acc = __fma_rn(brow[r], seg[r], acc);
+    out[jb.out_off + i] = acc;
+  }
+}
+
+hipError_t launch_lora_b(const LoraBJob* jobs, uint32_t njobs, uint32_t max_d_out, const double* sums, double* out,
+                         uint32_t cols, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  uint32_t bx = (max_d_out + 255) / 256;
+  if (bx > 64) bx = 64;
+  hipLaunchKernelGGL(k_lora_b, dim3(bx, njobs), dim3(256), 0, s, jobs, sums, out, cols);
+  return hipGetLastError();
+}
+
+}  // namespace th

@@ -237,6 +237,25 @@ __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], t
   }
 }
 
+// The operation fused into the coefficient load (NttLoad); `i` indexes the
+// limb-polynomial, so src, aux and key are read at the same position.
+struct LoadOp {
+  uint32_t kind;
+  const uint64_t* aux;
+  const uint64_t* key;  // secret-key limb-poly (DOT)
+  BarrettConst bc;
+  RescaleConst rc;
+  __device__ __forceinline__ uint64_t operator()(const uint64_t* __restrict__ src, uint32_t i) const {
+    const uint64_t x = src[i];
+    switch (kind) {
+      case NTT_LOAD_MUL: return mulmod_barrett(x, aux[i], bc);
+      case NTT_LOAD_RESCALE: return rescale_coeff(x, aux[i], rc);
+      case NTT_LOAD_DOT: return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
+      default: return x;
+    }
+  }
+};
+
 // Global access: lane-contiguous (element t + k*T) whenever LDS can restage
 // the whole polynomial in one round. With the two-round exchange (N = 32768)
 // the layout-0 <-> lane-contiguous restaging has no valid split bit, so the
@@ -244,7 +263,7 @@ __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], t
 // directly (each lane owns E consecutive words).
 template <int LOGN, bool INV, class A>
 __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                        const LimbConst& lc, void* lds_raw) {
+                                        const LimbConst& lc, const LoadOp& op, void* lds_raw) {
   using S = Shape<LOGN>;
   const uint32_t tid = threadIdx.x;
   const A ar(lc);
@@ -252,7 +271,7 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) x[k] = ar.load(src[tid + k * S::T]);
+    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, tid + k * S::T));
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
     fwd_passes<LOGN, LOGN, S::COAL_LO, true, A>(x, lds, tid, tw, ar);
     constexpr int OUT_LO = S::HALVES == 1 ? S::COAL_LO : 0;
@@ -261,7 +280,7 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
   } else {
     constexpr int IN_LO = S::HALVES == 1 ? S::COAL_LO : 0;
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) x[k] = ar.load(src[elem<S::LE, IN_LO>(tid, k)]);
+    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, IN_LO>(tid, k)));
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
     inv_passes<LOGN, 0, IN_LO, A>(x, lds, tid, tw, ar, lc);
 #pragma unroll
@@ -276,20 +295,28 @@ __global__ __launch_bounds__(Shape<LOGN>::T) void ntt_kernel(NttArgs a) {
   const uint64_t* src;
   uint64_t* dst;
   uint32_t limb;
+  LoadOp op{};
   if (a.jobs) {
-    src = a.jobs[job].src;
-    dst = a.jobs[job].dst;
-    limb = a.jobs[job].limb;
+    const NttJob jb = a.jobs[job];
+    src = jb.src;
+    dst = jb.dst;
+    limb = jb.limb;
+    op.kind = a.load;
+    op.aux = jb.aux;
+    if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
+    if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * Shape<LOGN>::N;
+    if (a.load == NTT_LOAD_RESCALE) op.rc = a.rc[limb];
   } else {
     src = a.src + (uint64_t)job * a.stride;
     dst = a.dst + (uint64_t)job * a.stride;
     limb = a.limb_base + job % a.limb_mod;
+    op.kind = NTT_LOAD_NONE;
   }
   const LimbConst& lc = a.lc[limb];
   if (lc.fp64)
-    run_ntt<LOGN, INV, Fp64Arith>(src, dst, lc, lds);
+    run_ntt<LOGN, INV, Fp64Arith>(src, dst, lc, op, lds);
   else
-    run_ntt<LOGN, INV, IntArith>(src, dst, lc, lds);
+    run_ntt<LOGN, INV, IntArith>(src, dst, lc, op, lds);
 }
 
 template <int LOGN, bool INV>

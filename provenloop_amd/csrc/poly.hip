@@ -6,10 +6,6 @@
 
 namespace th {
 
-__device__ __forceinline__ uint64_t addmod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
-__device__ __forceinline__ uint64_t submod(uint64_t a, uint64_t b, uint64_t q) {
-  return a >= b ? a - b : a + q - b;
-}
 // tensafe-he-core/src/ciphertext.rs:132-136: e >= 0 ? e % q : q - (|e| % q).
 // |e| < 2^63 < q^2 for every prime used, so the Barrett remainder is exact.
 __device__ __forceinline__ uint64_t signed_residue(int64_t e, const BarrettConst& m) {
@@ -80,40 +76,6 @@ __global__ void k_encrypt_combine(const EncCombineJob* __restrict__ jobs, const 
   }
 }
 
-// Rescale in the coefficient domain (ciphertext.rs:476-535): for every
-// component c and limb l < L-1,
-//   out[c][l] = ((x[c][l] - (x[c][L-1] mod q_l)) mod q_l) * (q_{L-1} mod q_l)^{-1}
-// where x is the inverse-transformed input ciphertext (2 x L limb-polys).
-__global__ void k_rescale_combine(const RescaleJob* __restrict__ jobs, const RescaleConst* __restrict__ rc,
-                                  uint32_t n, uint32_t L) {
-  const RescaleJob jb = jobs[blockIdx.y];
-  const uint32_t Lo = L - 1;
-  const uint32_t total = 2 * Lo * n;
-  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-    const uint32_t comp = e / (Lo * n);
-    const uint32_t w = e - comp * Lo * n;
-    const uint32_t l = w / n, i = w - l * n;
-    const RescaleConst c = rc[l];
-    const uint64_t x = jb.coef[((uint64_t)comp * L + l) * n + i];
-    const uint64_t last = jb.coef[((uint64_t)comp * L + Lo) * n + i];
-    const uint64_t lm = last < c.b.q ? last : mulmod_barrett(last, 1, c.b);
-    const uint64_t d = x >= lm ? x - lm : c.q - lm + x;
-    jb.out[e] = csub(shoup_lazy(d, c.inv, c.inv_s, c.q), c.q);
-  }
-}
-
-// m_l = c0_l + c1_l * s_l for the decrypted limbs l < nl (ciphertext.rs:332-341).
-__global__ void k_decrypt_dot(const DotJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
-                              const uint64_t* __restrict__ s, uint32_t n) {
-  const DotJob jb = jobs[blockIdx.y];
-  const uint32_t total = jb.nl * n;
-  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-    const uint32_t l = e / n;
-    const BarrettConst m = bc[l];
-    jb.out[e] = addmod(jb.c0[e], mulmod_barrett(jb.c1[e], s[e], m), m.q);
-  }
-}
-
 static dim3 grid_for(uint32_t elems, uint32_t jobs) {
   uint32_t bx = (elems + 255) / 256;
   if (bx > 64) bx = 64;
@@ -138,20 +100,6 @@ hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, con
                                   uint32_t n, uint32_t L, hipStream_t s) {
   if (!njobs) return hipSuccess;
   hipLaunchKernelGGL(k_encrypt_combine, grid_for(L * n, njobs), dim3(256), 0, s, jobs, bc, n, L);
-  return hipGetLastError();
-}
-
-hipError_t launch_rescale_combine(const RescaleJob* jobs, uint32_t njobs, const RescaleConst* rc, uint32_t n,
-                                  uint32_t L, hipStream_t s) {
-  if (!njobs) return hipSuccess;
-  hipLaunchKernelGGL(k_rescale_combine, grid_for(2 * (L - 1) * n, njobs), dim3(256), 0, s, jobs, rc, n, L);
-  return hipGetLastError();
-}
-
-hipError_t launch_decrypt_dot(const DotJob* jobs, uint32_t njobs, const BarrettConst* bc, const uint64_t* sk,
-                              uint32_t n, uint32_t max_nl, hipStream_t s) {
-  if (!njobs) return hipSuccess;
-  hipLaunchKernelGGL(k_decrypt_dot, grid_for(max_nl * n, njobs), dim3(256), 0, s, jobs, bc, sk, n);
   return hipGetLastError();
 }
 

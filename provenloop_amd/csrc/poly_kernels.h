@@ -28,24 +28,6 @@ struct EncCombineJob {
   uint64_t* out;         // [c0 | c1]
 };
 
-struct RescaleConst {
-  uint64_t q, inv, inv_s;  // (q_last mod q)^{-1} and its Shoup companion
-  BarrettConst b;          // remainder of a 64-bit value modulo q
-};
-
-struct RescaleJob {
-  const uint64_t* coef;  // inverse-transformed input, [c0 | c1] with L limbs each
-  uint64_t* out;         // [c0 | c1] with L-1 limbs each (coefficient domain)
-};
-
-struct DotJob {
-  const uint64_t* c0;
-  const uint64_t* c1;
-  uint64_t* out;  // nl limb-polys
-  uint32_t nl;    // limbs to decrypt (1, or 2 for the CRT branch)
-  uint32_t pad_;
-};
-
 struct DecodeConst {
   uint64_t q0, q1, half_q0;
   uint64_t q0_inv_q1, q0_inv_q1_s;  // (q0 mod q1)^{-1} mod q1, Shoup companion
@@ -63,16 +45,28 @@ struct DecodeJob {
   uint32_t pad_;
 };
 
+// delta = B @ intermediate for one LoRA projection. Rows of the LoRA-A side
+// are numbered so that row r's segment sum sits at sums[first_row * cols + r]
+// (batches of one projection are consecutive), which is the ZeRo-MOAI
+// extraction order (inference_engine.py:1379-1386).
+struct LoraBJob {
+  const double* b;     // d_out x rank, row-major
+  uint32_t d_out;
+  uint32_t rank;
+  uint32_t first_row;  // first plaintext batch of the projection
+  uint32_t pad_;
+  uint64_t out_off;    // offset of the projection's deltas in the output
+};
+
+hipError_t launch_lora_b(const LoraBJob* jobs, uint32_t njobs, uint32_t max_d_out, const double* sums, double* out,
+                         uint32_t cols, hipStream_t s);
+
 hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_limbs, const BarrettConst* bc,
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
                             uint32_t n, hipStream_t s);
 hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
                                   uint32_t n, uint32_t L, hipStream_t s);
-hipError_t launch_rescale_combine(const RescaleJob* jobs, uint32_t njobs, const RescaleConst* rc, uint32_t n,
-                                  uint32_t L, hipStream_t s);
-hipError_t launch_decrypt_dot(const DotJob* jobs, uint32_t njobs, const BarrettConst* bc, const uint64_t* sk,
-                              uint32_t n, uint32_t max_nl, hipStream_t s);
 hipError_t launch_signed_to_rns(const int64_t* x, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
                                hipStream_t s);
 hipError_t launch_sub_product(const uint64_t* x, const uint64_t* a, const uint64_t* sk, uint64_t* out,

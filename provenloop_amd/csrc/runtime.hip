@@ -192,6 +192,40 @@ struct th_pt {
   uint64_t* d;  // limbs x N
 };
 
+// A LoRA set: cached plaintext batches, LoRA-B matrices, one token's working
+// memory and the job lists of its launches, all in device memory taken from
+// the context pool (returned to it by th_lora_free).
+struct th_lora {
+  th_ctx* ctx;
+  uint32_t n_in = 0, d = 0, n_proj = 0, cols = 0, n_batches = 0, max_d_out = 0;
+  uint64_t n_deltas = 0;
+  std::vector<void*> owned;
+  uint64_t* pts = nullptr;     // n_batches x L x N, NTT domain
+  double* hidden = nullptr;    // n_in x d
+  uint8_t* u = nullptr;        // n_in x N
+  int64_t *e0 = nullptr, *e1 = nullptr;
+  uint64_t* prep = nullptr;    // n_in x 3L x N
+  uint64_t* cts = nullptr;     // n_in x 2L x N
+  uint64_t* work = nullptr;    // n_batches x 2L x N: rescale inverse transforms, or the products
+  uint64_t* res = nullptr;     // n_batches x 2(L-1) x N
+  uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
+  double* sums = nullptr;      // n_batches x cols
+  double* deltas = nullptr;    // n_deltas
+  SampleJob* d_sample = nullptr;
+  EncCombineJob* d_comb = nullptr;
+  const EncodeJob* d_enc = nullptr;
+  const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr, *d_dot_n = nullptr;
+  const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
+  const CtPtJob* d_ctpt = nullptr;
+  const LoraBJob* d_bjobs = nullptr;
+  uint32_t dot_n_jobs = 0, dot_r_jobs = 0;
+  void* alloc(size_t bytes) {
+    void* p = ctx->pool.get(bytes);
+    owned.push_back(p);
+    return p;
+  }
+};
+
 namespace {
 
 // Device buffers used by one API call (job lists, uploaded inputs, scratch).
@@ -278,12 +312,20 @@ void ntt_strided(th_ctx* c, bool inverse, const uint64_t* src, uint64_t* dst, ui
   HIPCHK(launch_ntt((int)c->logn, inverse, a, njobs, c->stream));
 }
 
-void ntt_list(OpScope& sc, bool inverse, const std::vector<NttJob>& jobs) {
+// Transforms of an explicit job list, with an optional operation fused into
+// the coefficient load (NttLoad): rc is the rescale-constant row of the
+// inputs' level (RESCALE), key the secret key (DOT).
+void ntt_list(OpScope& sc, bool inverse, const std::vector<NttJob>& jobs, NttLoad load = NTT_LOAD_NONE,
+              const RescaleConst* rc = nullptr, const uint64_t* key = nullptr) {
   th_ctx* c = sc.c;
   if (jobs.empty()) return;
   NttArgs a{};
   a.lc = c->d_lc;
   a.jobs = sc.up(jobs);
+  a.load = load;
+  a.bc = c->d_bc;
+  a.rc = rc;
+  a.key = key;
   HIPCHK(launch_ntt((int)c->logn, inverse, a, (uint32_t)jobs.size(), c->stream));
 }
 
@@ -555,7 +597,9 @@ std::vector<CtView> views_of(const th_ct* const* cts, size_t count) {
 }
 
 // Queue decrypt + decode of the views; slots to out_dev (count x S) and/or
-// segment sums to seg_dev (count x cols). Scratch lives in the caller's scope.
+// segment sums to seg_dev (count x cols). m_l = c0_l + c1_l * s_l
+// (ciphertext.rs:332-341) is formed inside the inverse transform's load.
+// Scratch lives in the caller's scope.
 void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk, double* out_dev, double* seg_dev,
                    uint32_t d, uint32_t cols) {
   th_ctx* c = sc.c;
@@ -563,18 +607,15 @@ void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk,
   const uint32_t N = c->N, S = N / 2;
   uint64_t* dot = (uint64_t*)sc.dev(count * 2 * poly_bytes(c));
   double* parts = (double*)sc.dev(count * decode_parts_doubles(c->logn) * 8);
-  std::vector<DotJob> dj(count);
   std::vector<NttJob> nj;
   std::vector<DecodeJob> dec(count);
-  uint32_t max_nl = 1;
   for (size_t i = 0; i < count; ++i) {
     const CtView& ct = cts[i];
     // ciphertext.rs:351: CRT branch iff scale > 1.5 * 2^40 and at least two limbs
     const uint32_t nl = (ct.scale > kScale * 1.5 && ct.limbs >= 2) ? 2 : 1;
-    max_nl = std::max(max_nl, nl);
     uint64_t* o = dot + i * 2 * N;
-    dj[i] = DotJob{ct.d, ct.d + (size_t)ct.limbs * N, o, nl, 0};
-    for (uint32_t l = 0; l < nl; ++l) nj.push_back(NttJob{o + (size_t)l * N, o + (size_t)l * N, l, 0});
+    for (uint32_t l = 0; l < nl; ++l)
+      nj.push_back(NttJob{ct.d + (size_t)l * N, o + (size_t)l * N, ct.d + (size_t)(ct.limbs + l) * N, l, 0});
     dec[i].m = o;
     dec[i].parts = parts + i * decode_parts_doubles(c->logn);
     dec[i].out = out_dev ? out_dev + i * S : nullptr;
@@ -582,8 +623,7 @@ void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk,
     dec[i].scale = ct.scale;
     dec[i].crt = nl == 2;
   }
-  HIPCHK(launch_decrypt_dot(sc.up(dj), (uint32_t)count, c->d_bc, sk->d, N, max_nl, c->stream));
-  ntt_list(sc, true, nj);
+  ntt_list(sc, true, nj, NTT_LOAD_DOT, nullptr, sk->d);
   HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
                        c->d_stage_im, c->logn, d, cols, c->stream));
 }
@@ -602,8 +642,13 @@ void queue_ct_pt(OpScope& sc, const std::vector<CtView>& in, const uint64_t* con
 }
 
 // Rescale (ciphertext.rs:476-535) of views that all have L >= 2 limbs into
-// out[i] (2 x (L-1) limb-polys each).
-void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* out) {
+// out[i] (2 x (L-1) limb-polys each): inverse NTT of every limb, then a
+// forward NTT of limbs 0..L-2 whose load forms
+// (c_l - (c_last mod q_l)) * (q_last mod q_l)^{-1}. With pts, input i is first
+// multiplied by pts[i] (ct_pt_mul_ntt, ciphertext.rs:422-429) inside the
+// inverse transform's load, so the product ciphertext is never stored.
+void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* out,
+                   const uint64_t* const* pts = nullptr) {
   th_ctx* c = sc.c;
   const uint32_t N = c->N;
   const size_t count = in.size();
@@ -613,16 +658,19 @@ void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* 
   inv.reserve(count * 2 * L);
   for (size_t i = 0; i < count; ++i)
     for (uint32_t k = 0; k < 2 * L; ++k)
-      inv.push_back(NttJob{in[i].d + (size_t)k * N, coef + (i * 2 * L + k) * N, k % L, 0});
-  ntt_list(sc, true, inv);
-  std::vector<RescaleJob> rj(count);
-  for (size_t i = 0; i < count; ++i) rj[i] = RescaleJob{coef + i * 2 * L * N, out[i]};
-  HIPCHK(launch_rescale_combine(sc.up(rj), (uint32_t)count, c->d_rc + (size_t)L * c->L, N, L, c->stream));
+      inv.push_back(NttJob{in[i].d + (size_t)k * N, coef + (i * 2 * L + k) * N,
+                           pts ? pts[i] + (size_t)(k % L) * N : nullptr, k % L, 0});
+  ntt_list(sc, true, inv, pts ? NTT_LOAD_MUL : NTT_LOAD_NONE);
   std::vector<NttJob> fwd;
   fwd.reserve(count * 2 * (L - 1));
   for (size_t i = 0; i < count; ++i)
-    for (uint32_t k = 0; k < 2 * (L - 1); ++k) fwd.push_back(NttJob{out[i] + (size_t)k * N, out[i] + (size_t)k * N, k % (L - 1), 0});
-  ntt_list(sc, false, fwd);
+    for (uint32_t comp = 0; comp < 2; ++comp) {
+      const uint64_t* cc = coef + (i * 2 + comp) * L * N;
+      for (uint32_t l = 0; l + 1 < L; ++l)
+        fwd.push_back(NttJob{cc + (size_t)l * N, out[i] + (size_t)(comp * (L - 1) + l) * N, cc + (size_t)(L - 1) * N,
+                             l, 0});
+    }
+  ntt_list(sc, false, fwd, NTT_LOAD_RESCALE, c->d_rc + (size_t)L * c->L);
 }
 
 void check_decrypt_args(th_ctx* c, const th_ct* const* cts, size_t count, const th_sk* sk) {
@@ -1227,27 +1275,302 @@ int th_lora_a_pass(th_ctx* ctx, const th_pk* pk, const th_sk* sk, const double* 
     for (uint32_t i = 0; i < n_inputs; ++i) ct_ptr[i] = cts + (size_t)i * 2 * L * N;
     queue_encrypt_pk(sc, pk, z, n_inputs, seeds, d, cols, ct_ptr.data());
     // products ct[pt_input[j]] x pts[j] (inference_engine.py:1311)
-    uint64_t* prods = (uint64_t*)sc.dev(n_pts * ctb);
     std::vector<CtView> in(n_pts), views(n_pts);
     std::vector<const uint64_t*> p(n_pts);
-    std::vector<uint64_t*> dst(n_pts);
     for (uint32_t j = 0; j < n_pts; ++j) {
       in[j] = CtView{ct_ptr[pt_input[j]], L, kScale};
       p[j] = pts[j]->d;
-      dst[j] = prods + (size_t)j * 2 * L * N;
-      views[j] = CtView{dst[j], L, kScale * kScale};
     }
-    queue_ct_pt(sc, in, p.data(), dst.data());
     if (do_rescale) {
+      // the product is formed inside the rescale's inverse transforms
       uint64_t* res = (uint64_t*)sc.dev(n_pts * 2 * (L - 1) * poly_bytes(ctx));
       std::vector<uint64_t*> rdst(n_pts);
       for (uint32_t j = 0; j < n_pts; ++j) rdst[j] = res + (size_t)j * 2 * (L - 1) * N;
-      queue_rescale(sc, views, rdst.data());
+      queue_rescale(sc, in, rdst.data(), p.data());
       for (uint32_t j = 0; j < n_pts; ++j) views[j] = CtView{rdst[j], L - 1, kScale * kScale / (double)ctx->q[L - 1]};
+    } else {
+      uint64_t* prods = (uint64_t*)sc.dev(n_pts * ctb);
+      std::vector<uint64_t*> dst(n_pts);
+      for (uint32_t j = 0; j < n_pts; ++j) {
+        dst[j] = prods + (size_t)j * 2 * L * N;
+        views[j] = CtView{dst[j], L, kScale * kScale};
+      }
+      queue_ct_pt(sc, in, p.data(), dst.data());
     }
     double* seg = (double*)sc.dev((size_t)n_pts * cols * 8);
     queue_decrypt(sc, views, sk, nullptr, seg, d, cols);
     download(ctx, out, seg, (size_t)n_pts * cols * 8);
+  });
+}
+
+}  // extern "C"
+
+namespace {
+
+// Device copy of a host vector that lives as long as the set.
+template <class T>
+const T* persist(th_lora* set, const std::vector<T>& v) {
+  th_ctx* c = set->ctx;
+  const size_t bytes = v.size() * sizeof(T);
+  T* d = (T*)set->alloc(bytes);
+  void* h = c->ring.reserve(bytes, c->stream);
+  memcpy(h, v.data(), bytes);
+  HIPCHK(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, c->stream));
+  return d;
+}
+
+void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, NttLoad load,
+                     const RescaleConst* rc = nullptr, const uint64_t* key = nullptr) {
+  NttArgs a{};
+  a.lc = c->d_lc;
+  a.jobs = jobs;
+  a.load = load;
+  a.bc = c->d_bc;
+  a.rc = rc;
+  a.key = key;
+  HIPCHK(launch_ntt((int)c->logn, inverse, a, n, c->stream));
+}
+
+void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, const uint32_t* d_out,
+                const double* const* a, const double* const* b) {
+  th_ctx* c = set->ctx;
+  const uint32_t N = c->N, S = N / 2, L = c->L, d = set->d, cols = set->cols;
+  const size_t P = poly_bytes(c);
+  // plaintext batches (inference_engine.py:1300-1308) and the B jobs
+  std::vector<double> packed;
+  std::vector<uint32_t> batch_input;
+  std::vector<LoraBJob> bj(set->n_proj);
+  std::vector<double> bmat;
+  uint64_t out_off = 0;
+  for (uint32_t j = 0; j < set->n_proj; ++j) {
+    const uint32_t nb = (ranks[j] + cols - 1) / cols;
+    bj[j] = LoraBJob{nullptr, d_out[j], ranks[j], (uint32_t)batch_input.size(), 0, out_off};
+    for (uint32_t bt = 0; bt < nb; ++bt) {
+      packed.resize(packed.size() + S, 0.0);
+      double* p = packed.data() + packed.size() - S;
+      for (uint32_t i = 0; i < cols && bt * cols + i < ranks[j]; ++i)
+        memcpy(p + (size_t)i * d, a[j] + (size_t)(bt * cols + i) * d, (size_t)d * 8);
+      batch_input.push_back(input_of[j]);
+    }
+    bmat.insert(bmat.end(), b[j], b[j] + (size_t)d_out[j] * ranks[j]);
+    out_off += d_out[j];
+    set->max_d_out = std::max(set->max_d_out, d_out[j]);
+  }
+  set->n_batches = (uint32_t)batch_input.size();
+  set->n_deltas = out_off;
+  const uint32_t nb = set->n_batches, ni = set->n_in;
+  const double* d_b = persist(set, bmat);
+  size_t boff = 0;
+  for (uint32_t j = 0; j < set->n_proj; ++j) {
+    bj[j].b = d_b + boff;
+    boff += (size_t)d_out[j] * ranks[j];
+  }
+  // device memory
+  set->pts = (uint64_t*)set->alloc(nb * L * P);
+  set->hidden = (double*)set->alloc((size_t)ni * d * 8);
+  set->u = (uint8_t*)set->alloc((size_t)ni * N);
+  set->e0 = (int64_t*)set->alloc((size_t)ni * N * 8);
+  set->e1 = (int64_t*)set->alloc((size_t)ni * N * 8);
+  set->prep = (uint64_t*)set->alloc(ni * 3 * L * P);
+  double* enc_parts = (double*)set->alloc(ni * encode_parts_doubles(c->logn) * 8);
+  set->cts = (uint64_t*)set->alloc(ni * 2 * L * P);
+  set->work = (uint64_t*)set->alloc(nb * 2 * L * P);
+  set->res = (uint64_t*)set->alloc(nb * 2 * (L > 1 ? L - 1 : 1) * P);
+  set->m = (uint64_t*)set->alloc(nb * 2 * P);
+  double* dec_parts = (double*)set->alloc(nb * decode_parts_doubles(c->logn) * 8);
+  set->sums = (double*)set->alloc((size_t)nb * cols * 8);
+  set->deltas = (double*)set->alloc(set->n_deltas * 8);
+  set->d_sample = (SampleJob*)set->alloc(ni * sizeof(SampleJob));
+  set->d_comb = (EncCombineJob*)set->alloc(ni * sizeof(EncCombineJob));
+  // encode the plaintext batches (th_encode_to_ntt of each packed vector)
+  {
+    OpScope sc(c);
+    const double* z = sc.up(packed);
+    queue_encode(sc, z, nb, nullptr, nullptr, nullptr, set->pts, (size_t)L * N);
+    ntt_strided(c, false, set->pts, set->pts, nb * L, L);
+    HIPCHK(hipStreamSynchronize(c->stream));  // the scope's buffers return to the pool
+  }
+  // per-token job lists
+  std::vector<EncodeJob> ej(ni);
+  for (uint32_t i = 0; i < ni; ++i) {
+    ej[i].z = set->hidden + (size_t)i * d;
+    ej[i].rep_d = d;
+    ej[i].rep_cols = cols;
+    ej[i].u = set->u + (size_t)i * N;
+    ej[i].e0 = set->e0 + (size_t)i * N;
+    ej[i].e1 = set->e1 + (size_t)i * N;
+    ej[i].dst = set->prep + (size_t)i * 3 * L * N;
+    ej[i].parts = enc_parts + i * encode_parts_doubles(c->logn);
+  }
+  set->d_enc = persist(set, ej);
+  std::vector<NttJob> inv, fwd, dot_r, dot_n;
+  std::vector<DecodeJob> dec_r(nb), dec_n(nb);
+  std::vector<CtPtJob> cp(nb);
+  const uint32_t Lr = L > 1 ? L - 1 : 1;
+  // decrypt branch (ciphertext.rs:351): CRT over limbs 0, 1 iff scale > 1.5 * 2^40 and >= 2 limbs
+  const double scale_n = kScale * kScale, scale_r = scale_n / (double)c->q[L - 1];
+  const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
+  const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
+  for (uint32_t bt = 0; bt < nb; ++bt) {
+    const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
+    const uint64_t* pt = set->pts + (size_t)bt * L * N;
+    uint64_t* w = set->work + (size_t)bt * 2 * L * N;
+    uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
+    uint64_t* mm = set->m + (size_t)bt * 2 * N;
+    for (uint32_t k = 0; k < 2 * L; ++k) inv.push_back(NttJob{ct + (size_t)k * N, w + (size_t)k * N, pt + (size_t)(k % L) * N, k % L, 0});
+    if (L >= 2) {
+      for (uint32_t comp = 0; comp < 2; ++comp)
+        for (uint32_t l = 0; l + 1 < L; ++l)
+          fwd.push_back(NttJob{w + (size_t)(comp * L + l) * N, r + (size_t)(comp * Lr + l) * N,
+                               w + (size_t)(comp * L + L - 1) * N, l, 0});
+      for (uint32_t l = 0; l < nl_r; ++l) dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(Lr + l) * N, l, 0});
+    }
+    for (uint32_t l = 0; l < nl_n; ++l) dot_n.push_back(NttJob{w + (size_t)l * N, mm + (size_t)l * N, w + (size_t)(L + l) * N, l, 0});
+    cp[bt] = CtPtJob{ct, ct + (size_t)L * N, pt, w, L, 0};
+    dec_r[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
+                          scale_r, nl_r == 2, 0};
+    dec_n[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
+                          scale_n, nl_n == 2, 0};
+  }
+  set->d_inv_mul = persist(set, inv);
+  if (L >= 2) {
+    set->d_fwd_rs = persist(set, fwd);
+    set->d_dot_r = persist(set, dot_r);
+    set->d_dec_r = persist(set, dec_r);
+  }
+  set->d_dot_n = persist(set, dot_n);
+  set->dot_n_jobs = (uint32_t)dot_n.size();
+  set->dot_r_jobs = (uint32_t)dot_r.size();
+  set->d_dec_n = persist(set, dec_n);
+  set->d_ctpt = persist(set, cp);
+  set->d_bjobs = persist(set, bj);
+  HIPCHK(hipStreamSynchronize(c->stream));
+}
+
+void free_lora(th_lora* set) {
+  for (void* p : set->owned) set->ctx->pool.put(p);
+  delete set;
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
+                   const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
+                   th_lora** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(out != nullptr, "null output");
+    need(n_inputs >= 1 && n_proj >= 1, "need at least one input and one projection");
+    need(d >= 1 && d <= ctx->N / 2, "d must be in [1, N/2]");
+    need(input_of && ranks && d_out && a && b, "null argument");
+    for (uint32_t j = 0; j < n_proj; ++j) {
+      need(input_of[j] < n_inputs, "input_of index out of range");
+      need(ranks[j] >= 1 && d_out[j] >= 1, "ranks and d_out must be positive");
+      need(a[j] && b[j], "null LoRA matrix");
+    }
+    th_lora* set = new th_lora{};
+    set->ctx = ctx;
+    set->n_in = n_inputs;
+    set->d = d;
+    set->n_proj = n_proj;
+    set->cols = (ctx->N / 2) / d;  // inference_engine.py:1258
+    try {
+      build_lora(set, input_of, ranks, d_out, a, b);
+    } catch (...) {
+      (void)hipStreamSynchronize(ctx->stream);
+      free_lora(set);
+      throw;
+    }
+    *out = set;
+  });
+}
+
+int th_lora_free(th_lora* set) {
+  return guarded([&] {
+    if (!set) return;
+    std::lock_guard<std::mutex> lk(set->ctx->mu);
+    use_device(set->ctx);
+    HIPCHK(hipStreamSynchronize(set->ctx->stream));
+    free_lora(set);
+  });
+}
+
+int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, uint32_t* cols) {
+  return guarded([&] {
+    need(set != nullptr, "null LoRA set");
+    if (n_deltas) *n_deltas = set->n_deltas;
+    if (n_batches) *n_batches = set->n_batches;
+    if (cols) *cols = set->cols;
+  });
+}
+
+int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
+                   int hidden_on_device, const uint64_t* seeds, int do_rescale, double* deltas,
+                   int deltas_on_device, double* inter) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(set && set->ctx == ctx, "LoRA set belongs to another context");
+    need(pk && pk->ctx == ctx && sk && sk->ctx == ctx, "keys belong to another context");
+    need(hidden && seeds && deltas, "null argument");
+    const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
+    need(!do_rescale || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
+    const size_t hbytes = (size_t)ni * set->d * 8;
+    hipStream_t st = ctx->stream;
+    if (hidden_on_device) {
+      HIPCHK(hipMemcpyAsync(set->hidden, hidden, hbytes, hipMemcpyDeviceToDevice, st));
+    } else {
+      void* h = ctx->ring.reserve(hbytes, st);
+      memcpy(h, hidden, hbytes);
+      HIPCHK(hipMemcpyAsync(set->hidden, h, hbytes, hipMemcpyHostToDevice, st));
+    }
+    // per-call jobs: the seeds and the public key
+    std::vector<SampleJob> sj(ni);
+    std::vector<EncCombineJob> cj(ni);
+    for (uint32_t i = 0; i < ni; ++i) {
+      sj[i] = SampleJob{seeds[i], set->u + (size_t)i * N, set->e0 + (size_t)i * N, set->e1 + (size_t)i * N};
+      cj[i] = EncCombineJob{set->prep + (size_t)i * 3 * L * N, pk->d, pk->d + (size_t)L * N,
+                            set->cts + (size_t)i * 2 * L * N};
+    }
+    const size_t sjb = ni * sizeof(SampleJob), cjb = ni * sizeof(EncCombineJob);
+    void* h = ctx->ring.reserve(sjb + cjb, st);
+    memcpy(h, sj.data(), sjb);
+    memcpy((char*)h + sjb, cj.data(), cjb);
+    HIPCHK(hipMemcpyAsync(set->d_sample, h, sjb, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(set->d_comb, (char*)h + sjb, cjb, hipMemcpyHostToDevice, st));
+    // encrypt_pk of every input (ciphertext.rs:240-319)
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st));
+    HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                         ctx->d_stage_im, ctx->logn, L, st));
+    ntt_strided(ctx, false, set->prep, set->prep, ni * 3 * L, L);
+    HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st));
+    if (do_rescale) {
+      // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
+      launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2 * L, NTT_LOAD_MUL);
+      launch_jobs_ntt(ctx, false, set->d_fwd_rs, nb * 2 * (L - 1), NTT_LOAD_RESCALE, ctx->d_rc + (size_t)L * L);
+      launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+      HIPCHK(launch_decode(set->d_dec_r, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
+    } else {
+      HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
+      launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+      HIPCHK(launch_decode(set->d_dec_n, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
+    }
+    double* dout = deltas_on_device ? deltas : set->deltas;
+    HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
+    const size_t db = set->n_deltas * 8, ib = (size_t)nb * set->cols * 8;
+    if (!deltas_on_device || inter) {
+      char* hh = (char*)ctx->ring.reserve(db + ib, st);
+      if (!deltas_on_device) HIPCHK(hipMemcpyAsync(hh, set->deltas, db, hipMemcpyDeviceToHost, st));
+      if (inter) HIPCHK(hipMemcpyAsync(hh + db, set->sums, ib, hipMemcpyDeviceToHost, st));
+      HIPCHK(hipStreamSynchronize(st));
+      if (!deltas_on_device) memcpy(deltas, hh, db);
+      if (inter) memcpy(inter, hh + db, ib);
+    } else {
+      HIPCHK(hipStreamSynchronize(st));
+    }
   });
 }
 

@@ -14,10 +14,16 @@ Restates the encrypted branch of the engine's `_he_lora_delta`
 
 Here all inputs of a token go through one encrypt_pk batch, all products
 through one launch, the optional rescale through one batch, and all
-decryptions through one GPU batch that returns only the segment sums.
+decryptions through one GPU batch that returns only the segment sums
+(`lora_deltas`, one th_lora_a_pass call). `LoraSet` keeps the plaintexts,
+the LoRA-B matrices and the token's working memory on the device and also
+applies B on the GPU (th_lora_create / th_lora_deltas), so a token is one
+call with one stream synchronisation and, if the caller keeps its hidden
+states and deltas in HBM, no host transfer at all.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 from dataclasses import dataclass, field
 from typing import Dict, List, Sequence
@@ -113,3 +119,88 @@ def lora_deltas(ctx: CkksContext, pk: TenSafePublicKey, sk: TenSafeSecretKey, hi
         vec[r0:r0 + n] = sums[row, :n]
     deltas = [[adapters[i][j].lora_b @ inter[(i, j)] for j in range(len(adapters[i]))] for i in range(len(adapters))]
     return deltas, inter
+
+
+class LoraSet:
+    """LoRA projections resident on the device (th_lora_create).
+
+    `projections` lists (input_index, lora_a [rank, d], lora_b [d_out, rank])
+    for every projection; projections that read the same input (q and v of
+    one layer) share that input's ciphertext. `deltas()` runs one token of
+    the encrypted path for all of them with one stream synchronisation:
+    encrypt_pk per input, ct x pt per packed batch, rescale, batched decrypt
+    with segment sums and B @ intermediate, all on the GPU.
+    """
+
+    def __init__(self, ctx: CkksContext, n_inputs: int, projections):
+        from . import _lib
+
+        self._ctx = ctx
+        self._lib = _lib.load()
+        projections = list(projections)
+        if not projections:
+            raise ValueError("need at least one projection")
+        self.n_inputs = int(n_inputs)
+        A = [np.ascontiguousarray(a, np.float64) for _, a, _ in projections]
+        B = [np.ascontiguousarray(b, np.float64) for _, _, b in projections]
+        d = A[0].shape[1]
+        for a, b in zip(A, B):
+            if a.ndim != 2 or a.shape[1] != d:
+                raise ValueError("every lora_a must be [rank, d] with the same d")
+            if b.ndim != 2 or b.shape[1] != a.shape[0]:
+                raise ValueError("lora_b must be [d_out, rank]")
+        self.d = d
+        self.d_out = [b.shape[0] for b in B]
+        self.offsets = np.concatenate([[0], np.cumsum(self.d_out)]).astype(int)
+        inp = np.array([int(i) for i, _, _ in projections], np.uint32)
+        ranks = np.array([a.shape[0] for a in A], np.uint32)
+        dout = np.array(self.d_out, np.uint32)
+        aptr = (C.c_void_p * len(A))(*[a.ctypes.data for a in A])
+        bptr = (C.c_void_p * len(B))(*[b.ctypes.data for b in B])
+        out = C.c_void_p()
+        _lib.check(self._lib.th_lora_create(ctx._h, self.n_inputs, d, len(A), _lib.ptr(inp), _lib.ptr(ranks),
+                                            _lib.ptr(dout), aptr, bptr, C.byref(out)))
+        self._h = out
+        nd, nb, cols = C.c_uint64(), C.c_uint32(), C.c_uint32()
+        _lib.check(self._lib.th_lora_info(self._h, C.byref(nd), C.byref(nb), C.byref(cols)))
+        self.n_deltas, self.n_batches, self.cols = nd.value, nb.value, cols.value
+
+    def __del__(self):
+        from . import _lib
+
+        h = getattr(self, "_h", None)
+        if h and _lib._lib is not None:
+            _lib._lib.th_lora_free(h)
+            self._h = None
+
+    def deltas(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden, seeds, rescale: bool = True,
+               with_intermediates: bool = False):
+        """Host in, host out: hidden [n_inputs, d] -> list of per-projection deltas."""
+        from . import _lib
+
+        H = np.ascontiguousarray(hidden, np.float64)
+        if H.shape != (self.n_inputs, self.d):
+            raise ValueError(f"hidden must be [{self.n_inputs}, {self.d}]")
+        sd = np.ascontiguousarray(seeds, np.uint64)
+        if sd.shape != (self.n_inputs,):
+            raise ValueError("need one seed per input")
+        out = np.empty(self.n_deltas, np.float64)
+        inter = np.empty((self.n_batches, self.cols), np.float64) if with_intermediates else None
+        _lib.check(self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk),
+                                            _lib.ptr(H), 0, _lib.ptr(sd), int(bool(rescale)), _lib.ptr(out), 0,
+                                            None if inter is None else _lib.ptr(inter)))
+        parts = [out[self.offsets[j]:self.offsets[j + 1]] for j in range(len(self.d_out))]
+        return (parts, inter) if with_intermediates else parts
+
+    def deltas_device(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden_dev: int, seeds, dev_out: int,
+                      rescale: bool = True):
+        """Device in, device out: hidden_dev points at n_inputs x d doubles in
+        HBM, dev_out receives n_deltas doubles; one stream synchronisation."""
+        from . import _lib
+
+        sd = np.ascontiguousarray(seeds, np.uint64)
+        if sd.shape != (self.n_inputs,):
+            raise ValueError("need one seed per input")
+        _lib.check(self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk),
+                                            C.c_void_p(hidden_dev), 1, _lib.ptr(sd), int(bool(rescale)),
+                                            C.c_void_p(dev_out), 1, None))

@@ -1,0 +1,196 @@
+"""LoRA sets (th_lora_create / th_lora_deltas): one token of the encrypted
+LoRA path for every projection, on the device, against the oracle.
+
+The oracle side composes the reference operations one by one
+(inference_engine.py:1258-1392 with the reference CKKS core): encrypt_pk of
+the replicated input, ct x pt with each packed batch, rescale, decrypt, sum
+of each d-slot segment, then B @ intermediate. Segment sums are reduced in a
+different order on the GPU, so they are held to 1e-9 absolute (relative to
+their size) and the deltas to the north-star 1e-3 relative bound (in
+practice ~1e-15); the ciphertext arithmetic under them is bit-exact (see
+test_gpu_parity.py), and the set's segment sums equal th_lora_a_pass's bit
+for bit.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from provenloop_amd import _lib, tensafe_he, zero_moai
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env():
+    eng, ref = tensafe_he.CkksContext(16384), orc.Context(16384)
+    sk, rsk = eng.keygen(seed=41), ref.keygen(41)
+    pk, rpk = eng.keygen_public(sk, seed=42), ref.keygen_public(rsk, 42)
+    return eng, ref, sk, pk, rsk, rpk
+
+
+def _oracle(ref, rpk, rsk, H, seeds, projections, rescale):
+    S = ref.num_slots
+    d = H.shape[1]
+    cols = S // d
+    cts = [ref.encrypt_pk(zero_moai.replicate(h, S, d), rpk, int(sd)) for h, sd in zip(H, seeds)]
+    deltas, sums = [], []
+    for i, A, B in projections:
+        inter = np.zeros(A.shape[0])
+        for b, p in enumerate(zero_moai.pack_rows(A, S)):
+            r = ref.ct_pt_mul(cts[i], p)
+            if rescale:
+                r = ref.rescale(r)
+            dec = ref.decrypt(r, rsk)
+            seg = np.array([np.sum(dec[c * d:(c + 1) * d]) for c in range(cols)])
+            sums.append(seg)
+            n = min(cols, A.shape[0] - b * cols)
+            inter[b * cols:b * cols + n] = seg[:n]
+        deltas.append(B @ inter)
+    return deltas, np.array(sums)
+
+
+def _check(got, got_sums, exp, exp_sums):
+    assert got_sums.shape == exp_sums.shape
+    assert np.max(np.abs(got_sums - exp_sums)) <= 1e-9 * max(1.0, np.max(np.abs(exp_sums)))
+    for g, e in zip(got, exp):
+        assert g.shape == e.shape
+        assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e)
+        assert np.max(np.abs(g - e)) <= 1e-9 * max(1.0, np.max(np.abs(e)))
+
+
+def _projections(rng, n_inputs, d, ranks, d_outs):
+    return [(j % n_inputs, rng.normal(size=(r, d)) * 0.02, rng.normal(size=(o, r)) * 0.02)
+            for j, (r, o) in enumerate(zip(ranks, d_outs))]
+
+
+@pytest.mark.parametrize("rescale", [True, False])
+def test_lora_set_matches_oracle(env, rescale):
+    """Two layers x {q, v} at the Qwen2.5-1.5B shape (d=1536, rank 16, B_q 1536x16, B_v 256x16)."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(7)
+    H = rng.normal(size=(2, 1536)) * 0.1
+    proj = [(l, rng.normal(size=(16, 1536)) * 0.02, rng.normal(size=(o, 16)) * 0.02)
+            for l in range(2) for o in (1536, 256)]
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    assert (ls.n_batches, ls.cols, ls.n_deltas) == (16, 5, 2 * (1536 + 256))
+    seeds = [9001, 9002]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=rescale, with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, rescale)
+    _check(got, got_sums, exp, exp_sums)
+    # the same segment sums as th_lora_a_pass (same kernels), bit for bit
+    pts = [eng.encode_to_ntt(p) for _, A, _ in proj for p in zero_moai.pack_rows(A, 8192)]
+    pin = [i for i, A, _ in proj for _ in range(4)]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=rescale), got_sums)
+
+
+def test_lora_set_ragged_shapes(env):
+    """Ranks that do not fill the last batch, d with cols = 8, uneven d_out, inputs shared unevenly."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(8)
+    d = 1000
+    H = rng.normal(size=(3, d)) * 0.1
+    proj = _projections(rng, 3, d, ranks=[3, 13, 8, 1], d_outs=[7, 300, 1, 64])
+    ls = zero_moai.LoraSet(eng, 3, proj)
+    assert ls.cols == 8 and ls.n_batches == 1 + 2 + 1 + 1
+    seeds = [1, 2, 3]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, True)
+    _check(got, got_sums, exp, exp_sums)
+
+
+def test_lora_set_one_column_per_batch(env):
+    """d > N/4: one segment per plaintext batch (cols = 1)."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(9)
+    d = 5000
+    H = rng.normal(size=(1, d)) * 0.1
+    proj = _projections(rng, 1, d, ranks=[3], d_outs=[5])
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    assert ls.cols == 1 and ls.n_batches == 3
+    got, got_sums = ls.deltas(pk, sk, H, [77], with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, [77], proj, True)
+    _check(got, got_sums, exp, exp_sums)
+
+
+def test_lora_set_device_io_matches_host_io(env):
+    eng, ref, sk, pk, rsk, rpk = env
+    L = _lib.load()
+    rng = np.random.default_rng(10)
+    H = rng.normal(size=(2, 1536)) * 0.1
+    proj = _projections(rng, 2, 1536, ranks=[16, 16, 16], d_outs=[1536, 256, 100])
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    host = np.concatenate(ls.deltas(pk, sk, H, [5, 6]))
+    hd, od = C.c_void_p(), C.c_void_p()
+    _lib.check(L.th_dev_alloc(eng._h, H.nbytes, C.byref(hd)))
+    _lib.check(L.th_dev_alloc(eng._h, ls.n_deltas * 8, C.byref(od)))
+    try:
+        Hc = np.ascontiguousarray(H)
+        _lib.check(L.th_memcpy_h2d(eng._h, hd, _lib.ptr(Hc), H.nbytes))
+        for _ in range(2):  # the set's working memory is reused across tokens
+            ls.deltas_device(pk, sk, hd.value, [5, 6], od.value)
+            dev = np.empty(ls.n_deltas)
+            _lib.check(L.th_memcpy_d2h(eng._h, _lib.ptr(dev), od, ls.n_deltas * 8))
+            assert np.array_equal(dev, host)
+    finally:
+        _lib.check(L.th_dev_free(eng._h, hd))
+        _lib.check(L.th_dev_free(eng._h, od))
+
+
+def test_lora_set_tokens_are_independent(env):
+    """A later token with other inputs and seeds gives its own result (no stale working memory)."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(11)
+    proj = _projections(rng, 1, 1536, ranks=[16], d_outs=[64])
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    H1, H2 = rng.normal(size=(1, 1536)) * 0.1, rng.normal(size=(1, 1536)) * 0.1
+    a = ls.deltas(pk, sk, H1, [1])[0]
+    b = ls.deltas(pk, sk, H2, [2])[0]
+    a2 = ls.deltas(pk, sk, H1, [1])[0]
+    assert np.array_equal(a, a2) and not np.array_equal(a, b)
+    exp, _ = _oracle(ref, rpk, rsk, H2, [2], proj, True)
+    assert np.linalg.norm(b - exp[0]) <= 1e-3 * np.linalg.norm(exp[0])
+
+
+def test_lora_set_argument_errors(env):
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(12)
+    proj = _projections(rng, 1, 1536, ranks=[4], d_outs=[8])
+    with pytest.raises(ValueError, match="input_of"):
+        zero_moai.LoraSet(eng, 1, [(1,) + proj[0][1:]])
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    with pytest.raises(ValueError):
+        ls.deltas(pk, sk, np.zeros((2, 1536)), [1])
+    one = tensafe_he.CkksContext(16384, moduli=[1152921504606748673])
+    osk = one.keygen(seed=1)
+    opk = one.keygen_public(osk, seed=2)
+    ols = zero_moai.LoraSet(one, 1, proj)
+    with pytest.raises(RuntimeError, match="Cannot rescale"):
+        ols.deltas(opk, osk, np.zeros((1, 1536)), [1], rescale=True)
+    with pytest.raises(ValueError, match="another context"):
+        ols.deltas(pk, sk, np.zeros((1, 1536)), [1], rescale=False)
+    # one limb without rescale: the non-CRT decrypt branch
+    oref = orc.Context(16384, moduli=[1152921504606748673])
+    orsk = oref.keygen(1)
+    orpk = oref.keygen_public(orsk, 2)
+    H = rng.normal(size=(1, 1536)) * 0.1
+    got, got_sums = ols.deltas(opk, osk, H, [3], rescale=False, with_intermediates=True)
+    exp, exp_sums = _oracle(oref, orpk, orsk, H, [3], proj, False)
+    _check(got, got_sums, exp, exp_sums)
+
+
+def test_lora_set_crt_branch_after_rescale():
+    """A chain whose last prime is 30-bit: the rescaled scale is ~2^50 > 1.5 * 2^40, so the
+    decrypt takes the CRT branch over limbs 0 and 1 (ciphertext.rs:351)."""
+    q = [1152921504606748673, 1099510054913, 1073643521]
+    eng, ref = tensafe_he.CkksContext(16384, moduli=q), orc.Context(16384, moduli=q)
+    sk, rsk = eng.keygen(seed=3), ref.keygen(3)
+    pk, rpk = eng.keygen_public(sk, seed=4), ref.keygen_public(rsk, 4)
+    rng = np.random.default_rng(13)
+    H = rng.normal(size=(1, 1536)) * 0.1
+    proj = _projections(rng, 1, 1536, ranks=[16], d_outs=[32])
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    got, got_sums = ls.deltas(pk, sk, H, [21], with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, [21], proj, True)
+    _check(got, got_sums, exp, exp_sums)
