@@ -9,6 +9,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import re
+import sys
 
 import numpy as np
 
@@ -98,6 +99,25 @@ def header_symbols(path: str = HEADER_PATH) -> list[str]:
     return sorted(set(re.findall(r"\b(th_[a-z0-9_]+)\s*\(", text)))
 
 
+def _share_hip_runtime_with_torch():
+    """Make the library and PyTorch use ONE HIP runtime in this process.
+
+    PyTorch-ROCm wheels carry their own libamdhip64 / libhsa-runtime64 and
+    load them under the unversioned name, while this library links the
+    system ROCm's libamdhip64.so.7. Loaded in that order, a process would hold
+    two HIP runtimes and the second to initialise finds no GPU. PyTorch's copy
+    has the same soname (libamdhip64.so.7), so importing torch first lets the
+    dynamic loader bind this library to the runtime already in the process.
+    Without torch installed the system runtime is used.
+    """
+    if "torch" in sys.modules:
+        return
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load():
     """Load the library (raises if it has not been built)."""
     global _lib
@@ -107,6 +127,7 @@ def load():
         raise HipEngineError(
             f"{LIB_PATH} is missing: build it with `make -C provenloop_amd/csrc` "
             "(or __graft_entry__.build()); there is no CPU fallback")
+    _share_hip_runtime_with_torch()
     L = C.CDLL(LIB_PATH)
     for name, (res, args) in _SIGS.items():
         f = getattr(L, name)

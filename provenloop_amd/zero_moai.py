@@ -30,6 +30,7 @@ from typing import Dict, List, Sequence
 
 import numpy as np
 
+from . import _lib
 from .tensafe_he import CkksContext, TenSafePlaintext, TenSafePublicKey, TenSafeSecretKey
 
 
@@ -133,8 +134,6 @@ class LoraSet:
     """
 
     def __init__(self, ctx: CkksContext, n_inputs: int, projections):
-        from . import _lib
-
         self._ctx = ctx
         self._lib = _lib.load()
         projections = list(projections)
@@ -166,8 +165,6 @@ class LoraSet:
         self.n_deltas, self.n_batches, self.cols = nd.value, nb.value, cols.value
 
     def __del__(self):
-        from . import _lib
-
         h = getattr(self, "_h", None)
         if h and _lib._lib is not None:
             _lib._lib.th_lora_free(h)
@@ -176,8 +173,6 @@ class LoraSet:
     def deltas(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden, seeds, rescale: bool = True,
                with_intermediates: bool = False):
         """Host in, host out: hidden [n_inputs, d] -> list of per-projection deltas."""
-        from . import _lib
-
         H = np.ascontiguousarray(hidden, np.float64)
         if H.shape != (self.n_inputs, self.d):
             raise ValueError(f"hidden must be [{self.n_inputs}, {self.d}]")
@@ -196,8 +191,6 @@ class LoraSet:
                       rescale: bool = True):
         """Device in, device out: hidden_dev points at n_inputs x d doubles in
         HBM, dev_out receives n_deltas doubles; one stream synchronisation."""
-        from . import _lib
-
         sd = np.ascontiguousarray(seeds, np.uint64)
         if sd.shape != (self.n_inputs,):
             raise ValueError("need one seed per input")

@@ -95,3 +95,14 @@ def test_adapter_init_fails_loudly_without_gpu():
         pytest.skip("a GPU is visible")
     with pytest.raises(_lib.HipEngineError, match="no HIP device"):
         adapter.init_tensafe_he(16384)
+
+
+def test_one_hip_runtime_per_process():
+    """The library binds to the HIP runtime PyTorch already loaded (same soname), so a
+    process using both never holds two runtimes (the second would find no GPU)."""
+    import re
+
+    _lib.load()
+    maps = open("/proc/self/maps").read()
+    assert len(set(re.findall(r"/\S*/libamdhip64\.so\S*", maps))) == 1
+    assert len(set(re.findall(r"/\S*/libhsa-runtime64\.so\S*", maps))) == 1

@@ -168,7 +168,7 @@ def test_lora_set_argument_errors(env):
     ols = zero_moai.LoraSet(one, 1, proj)
     with pytest.raises(RuntimeError, match="Cannot rescale"):
         ols.deltas(opk, osk, np.zeros((1, 1536)), [1], rescale=True)
-    with pytest.raises(ValueError, match="another context"):
+    with pytest.raises(ValueError, match="different CkksContext|another context"):
         ols.deltas(pk, sk, np.zeros((1, 1536)), [1], rescale=False)
     # one limb without rescale: the non-CRT decrypt branch
     oref = orc.Context(16384, moduli=[1152921504606748673])
