@@ -1,0 +1,103 @@
+// Butterfly arithmetic and load-side operations shared by the NTT kernels.
+//
+// Two exact modular-multiply policies (chosen per limb prime):
+//  IntArith  - 64-bit Shoup products with Harvey's lazy ranges
+//              ([0, 4q) forward, [0, 2q) inverse); any q < 2^62.
+//  Fp64Arith - q < 2^41: exact products from one FMA split and a quotient
+//              rounded from x * (w / q); values are exact integers in doubles.
+// Both end on the canonical residue, so transforms are bit-identical to the
+// reference's u128 Barrett NTT (tensafe-he-core/src/ntt.rs:79-141).
+// raw()/unraw() carry a policy's intermediate values through global memory
+// between the two kernels of a split transform (u64 lazy residues, or the
+// bit pattern of the double).
+#pragma once
+#include "th_internal.h"
+
+namespace th {
+
+// ------------------------------------------------------------------ arithmetic policies
+struct IntArith {
+  using V = uint64_t;
+  using Tw = ShoupTw;
+  uint64_t q, two_q;
+  __device__ IntArith(const LimbConst& c) : q(c.q), two_q(c.two_q) {}
+  __device__ __forceinline__ V load(uint64_t x) const { return x; }
+  // forward CT butterfly, inputs/outputs in [0, 4q)
+  __device__ __forceinline__ void fwd(V& a, V& b, const Tw& t) const {
+    uint64_t X = csub(a, two_q);
+    uint64_t T = shoup_lazy(b, t.w, t.ws, q);
+    a = X + T;
+    b = X + two_q - T;
+  }
+  // inverse GS butterfly, inputs/outputs in [0, 2q)
+  __device__ __forceinline__ void inv(V& a, V& b, const Tw& t) const {
+    uint64_t X = a, Y = b;
+    a = csub(X + Y, two_q);
+    b = shoup_lazy(X + two_q - Y, t.w, t.ws, q);
+  }
+  __device__ __forceinline__ void inv_last(V& a, V& b, const LimbConst& c) const {
+    uint64_t X = a, Y = b;
+    a = csub(shoup_lazy(X + Y, c.n_inv, c.n_inv_s, q), q);
+    b = csub(shoup_lazy(X + two_q - Y, c.last_w, c.last_ws, q), q);
+  }
+  __device__ __forceinline__ void inv_pass_end(V&) const {}
+  __device__ __forceinline__ uint64_t fwd_store(V x) const { return csub(csub(x, two_q), q); }
+  __device__ __forceinline__ uint64_t inv_store(V x) const { return x; }
+  __device__ __forceinline__ uint64_t raw(V x) const { return x; }
+  __device__ __forceinline__ V unraw(uint64_t x) const { return x; }
+};
+
+struct Fp64Arith {
+  using V = double;
+  using Tw = Fp64Tw;
+  double q, qinv;
+  __device__ Fp64Arith(const LimbConst& c) : q(c.qd), qinv(c.qinv) {}
+  __device__ __forceinline__ V load(uint64_t x) const { return u64_to_f64(x); }
+  // values grow by at most 0.51 q per stage; no reduction needed inside the transform
+  __device__ __forceinline__ void fwd(V& a, V& b, const Tw& t) const {
+    double X = a;
+    double T = mulmod_f64(b, t.w, t.wq, q);
+    a = X + T;
+    b = X - T;
+  }
+  // the sum doubles per stage: reduced at the end of every register pass
+  __device__ __forceinline__ void inv(V& a, V& b, const Tw& t) const {
+    double X = a, Y = b;
+    a = X + Y;
+    b = mulmod_f64(X - Y, t.w, t.wq, q);
+  }
+  __device__ __forceinline__ void inv_last(V& a, V& b, const LimbConst& c) const {
+    double X = a, Y = b;
+    double r0 = mulmod_f64(X + Y, c.n_inv_d, c.n_inv_dq, q);
+    double r1 = mulmod_f64(X - Y, c.last_wd, c.last_wdq, q);
+    a = r0 < 0.0 ? r0 + q : r0;
+    b = r1 < 0.0 ? r1 + q : r1;
+  }
+  __device__ __forceinline__ void inv_pass_end(V& x) const { x = reduce_f64_signed(x, q, qinv); }
+  __device__ __forceinline__ uint64_t fwd_store(V x) const { return f64_to_u64(reduce_f64(x, q, qinv)); }
+  __device__ __forceinline__ uint64_t inv_store(V x) const { return f64_to_u64(x); }
+  __device__ __forceinline__ uint64_t raw(V x) const { return __builtin_bit_cast(uint64_t, x); }
+  __device__ __forceinline__ V unraw(uint64_t x) const { return __builtin_bit_cast(double, x); }
+};
+
+// The operation fused into the coefficient load (NttLoad); `i` indexes the
+// limb-polynomial, so src, aux and key are read at the same position.
+struct LoadOp {
+  uint32_t kind;
+  const uint64_t* aux;
+  const uint64_t* key;  // secret-key limb-poly (DOT)
+  BarrettConst bc;
+  RescaleConst rc;
+  __device__ __forceinline__ uint64_t operator()(const uint64_t* __restrict__ src, uint32_t i) const {
+    const uint64_t x = src[i];
+    switch (kind) {
+      case NTT_LOAD_MUL: return mulmod_barrett(x, aux[i], bc);
+      case NTT_LOAD_RESCALE: return rescale_coeff(x, aux[i], rc);
+      case NTT_LOAD_DOT: return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
+      default: return x;
+    }
+  }
+};
+
+
+}  // namespace th

@@ -1,0 +1,264 @@
+// Split negacyclic NTT for N = 2^13 .. 2^15: a column pass and a row pass,
+// each one launch of single-wavefront workgroups.
+//
+// The coefficient index j = (row << CB) | col splits into CB low "column"
+// bits and RB = log N - CB high "row" bits. Every butterfly pairs two
+// indices that differ in one bit b, and its twiddle is (N + j) >> (b + 1)
+// for the lower index j (tensafe-he-core/src/ntt.rs:79-141, SEAL-style
+// tables). Stages on row bits only mix coefficients of one column; stages on
+// column bits only mix coefficients of one row. So
+//   forward = column pass (row bits, high to low) then row pass (column bits),
+//   inverse = row pass (column bits, low to high) then column pass (row bits,
+//             ending with the stage that folds in N^{-1}),
+// with no extra twiddle factors between the passes.
+//
+// Each wavefront owns 1024 coefficients of one limb-polynomial (16 per
+// lane), runs two register passes of up to four butterfly stages, and
+// re-distributes its coefficients between them through a private 8.5 KiB
+// LDS slice (no workgroup barrier beyond its own wavefront). Small LDS and
+// register footprints let many wavefronts share a CU, so global loads,
+// stores and arithmetic of different wavefronts overlap. The first pass
+// writes its intermediate values in the arithmetic's own representation
+// (lazy u64 residues, or f64 bit patterns) to the destination, where the
+// second pass reads them back, in the natural coefficient order. Every
+// workgroup reads and writes exactly the same set of positions in each pass
+// (its columns, or its rows), so a transform may run in place and no
+// workgroup can overwrite data another one has still to read.
+//
+// Wavefront layouts (l = lane, k = register, e = index within the
+// wavefront's 1024 coefficients):
+//   column pass, CW = 2^(10-RB) adjacent columns x all 2^RB rows:
+//     Q1: col = l mod CW, row = (l / CW) | (k << (RB-4))     registers = row bits [RB-4, RB)
+//     Q2: col = l mod CW, row = k | ((l / CW) << 4)           registers = row bits [0, 4)
+//   row pass, 2^(10-CB) adjacent rows x 2^CB columns:
+//     P1: col = (l mod 2^(CB-4)) | (k << (CB-4))              registers = col bits [CB-4, CB)
+//     P2: col = k | ((l mod 2^(CB-4)) << 4)                   registers = col bits [0, 4)
+//     G:  e = l + 64 k                                        (lane-contiguous global access)
+// Column-pass wavefronts 2m and 2m+1 share the 128-byte lines of the
+// natural layout; they are given workgroup ids that the dispatcher sends to
+// the same XCD (ids are dealt round-robin over the 8 XCDs), so the second
+// half of each line is served by that XCD's L2.
+#include "ntt_arith.h"
+
+namespace th {
+
+template <int LOGN>
+struct Split {
+  static constexpr int N = 1 << LOGN;
+  static constexpr int CB = LOGN >= 15 ? 8 : 7;  // column bits
+  static constexpr int RB = LOGN - CB;           // row bits
+  static constexpr int E = 16;
+  static constexpr int PARTS = N >> 10;          // wavefronts per limb-polynomial
+  static constexpr int CW = 1 << (10 - RB);      // columns per column-pass wavefront
+  static constexpr int LDS = 1024 + 64;          // one padding word per 16
+  static_assert(CB >= 4 && RB >= 4 && RB <= 10 && CB <= 10, "unsupported split");
+};
+
+__device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
+
+// Forward stages BHI down to BLO on registers that hold index bits
+// [EB, EB + 4); f = index of register 0 (its register bits are zero).
+template <int LOGN, int EB, int BHI, int BLO, class A>
+__device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, const typename A::Tw* __restrict__ tw,
+                                           const A& ar) {
+#pragma unroll
+  for (int b = BHI; b >= BLO; --b) {
+    const int rb = b - EB;
+    const uint32_t base = ((1u << LOGN) | f) >> (b + 1);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & (1 << rb)) continue;
+      const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+      ar.fwd(x[k], x[k | (1 << rb)], t);
+    }
+  }
+}
+
+// Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
+template <int LOGN, int EB, int BLO, int BHI, class A>
+__device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, const typename A::Tw* __restrict__ tw,
+                                           const A& ar, const LimbConst& lc) {
+#pragma unroll
+  for (int b = BLO; b <= BHI; ++b) {
+    const int rb = b - EB;
+    const uint32_t base = ((1u << LOGN) | f) >> (b + 1);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & (1 << rb)) continue;
+      if (b == LOGN - 1) {
+        ar.inv_last(x[k], x[k | (1 << rb)], lc);
+      } else {
+        const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+        ar.inv(x[k], x[k | (1 << rb)], t);
+      }
+    }
+  }
+  if (BHI != LOGN - 1) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ar.inv_pass_end(x[k]);
+  }
+}
+
+// Re-distribute the wavefront's 16 x 64 coefficients from layout `from` to
+// layout `to` (functions of the register index giving the index e in
+// [0, 1024)) through its LDS slice.
+template <class V, class From, class To>
+__device__ __forceinline__ void wave_exchange(V (&x)[16], V* lds, From from, To to) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) lds[pad16(from(k))] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = lds[pad16(to(k))];
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------ column pass
+template <int LOGN, bool INV, class A>
+__device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                            const LimbConst& lc, const LoadOp& op, uint32_t part, uint64_t* lds_raw) {
+  using S = Split<LOGN>;
+  constexpr int RB = S::RB, CB = S::CB, CW = S::CW, WL = 10 - RB;  // WL = log2(CW)
+  const uint32_t l = threadIdx.x;
+  const uint32_t lcol = l & (CW - 1), lrow = l >> WL;
+  const uint32_t col = part * CW + lcol;
+  // Q1 and Q2 element maps: local e = (row << WL) | lcol, global j = (row << CB) | col
+  auto row1 = [&](uint32_t k) { return lrow | (k << (RB - 4)); };
+  auto row2 = [&](uint32_t k) { return k | (lrow << 4); };
+  auto e1 = [&](uint32_t k) { return (row1(k) << WL) | lcol; };
+  auto e2 = [&](uint32_t k) { return (row2(k) << WL) | lcol; };
+  const A ar(lc);
+  typename A::V x[16];
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  if constexpr (!INV) {
+    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, (row1(k) << CB) | col));
+    fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4>(x, (row1(0) << CB) | col, tw, ar);
+    wave_exchange(x, lds, e1, e2);
+    fwd_stages<LOGN, CB, LOGN - 5, CB>(x, (row2(0) << CB) | col, tw, ar);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dst[(row2(k) << CB) | col] = ar.raw(x[k]);
+  } else {
+    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(dst[(row2(k) << CB) | col]);
+    inv_stages<LOGN, CB, CB, CB + 3>(x, (row2(0) << CB) | col, tw, ar, lc);
+    wave_exchange(x, lds, e2, e1);
+    inv_stages<LOGN, LOGN - 4, CB + 4, LOGN - 1>(x, (row1(0) << CB) | col, tw, ar, lc);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dst[(row1(k) << CB) | col] = ar.inv_store(x[k]);
+  }
+}
+
+// ------------------------------------------------------------------ row pass
+template <int LOGN, bool INV, class A>
+__device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                         const LimbConst& lc, const LoadOp& op, uint32_t part, uint64_t* lds_raw) {
+  using S = Split<LOGN>;
+  constexpr int CB = S::CB, M = (1 << (CB - 4)) - 1;
+  const uint32_t l = threadIdx.x;
+  const uint32_t jbase = part << 10;
+  const uint32_t rowbits = (l >> (CB - 4)) << CB;
+  auto p1 = [&](uint32_t k) { return (l & M) | (k << (CB - 4)) | rowbits; };
+  auto p2 = [&](uint32_t k) { return k | ((l & M) << 4) | rowbits; };
+  auto g = [&](uint32_t k) { return l + 64 * k; };
+  const A ar(lc);
+  typename A::V x[16];
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  if constexpr (!INV) {
+    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(dst[jbase + p1(k)]);
+    fwd_stages<LOGN, CB - 4, CB - 1, CB - 4>(x, jbase + p1(0), tw, ar);
+    wave_exchange(x, lds, p1, p2);
+    fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
+    wave_exchange(x, lds, p2, g);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dst[jbase + g(k)] = ar.fwd_store(x[k]);
+  } else {
+    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
+    wave_exchange(x, lds, g, p2);
+    inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+    wave_exchange(x, lds, p2, p1);
+    inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dst[jbase + p1(k)] = ar.raw(x[k]);
+  }
+}
+
+// ------------------------------------------------------------------ kernels
+// Workgroup b works on part b % PARTS of job b / PARTS. The pass that reads
+// the transform's input applies the fused load operation; the other pass
+// reads and writes the destination only.
+template <int LOGN, bool INV, bool COLUMN>
+__global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
+  using S = Split<LOGN>;
+  __shared__ uint64_t lds[S::LDS];
+  const uint32_t job = blockIdx.x / S::PARTS;
+  uint32_t part = blockIdx.x % S::PARTS;
+  if constexpr (COLUMN && S::CW < 16) {
+    // 8-column parts share 128-byte lines in pairs; ids i and i + 8 run on one
+    // XCD, so they get the column parts 2m and 2m + 1
+    static_assert(S::CW == 8 && S::PARTS % 16 == 0, "column-part pairing needs 8 columns and 16 | PARTS");
+    part = (part & ~15u) | ((part & 7u) << 1) | ((part >> 3) & 1u);
+  }
+  const uint64_t* src;
+  uint64_t* dst;
+  uint32_t limb;
+  LoadOp op{};
+  if (a.jobs) {
+    const NttJob jb = a.jobs[job];
+    src = jb.src;
+    dst = jb.dst;
+    limb = jb.limb;
+    op.kind = a.load;
+    op.aux = jb.aux;
+    if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
+    if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * S::N;
+    if (a.load == NTT_LOAD_RESCALE) op.rc = a.rc[limb];
+  } else {
+    src = a.src + (uint64_t)job * a.stride;
+    dst = a.dst + (uint64_t)job * a.stride;
+    limb = a.limb_base + job % a.limb_mod;
+    op.kind = NTT_LOAD_NONE;
+  }
+  const LimbConst& lc = a.lc[limb];
+  if constexpr (COLUMN) {
+    if (lc.fp64)
+      column_pass<LOGN, INV, Fp64Arith>(src, dst, lc, op, part, lds);
+    else
+      column_pass<LOGN, INV, IntArith>(src, dst, lc, op, part, lds);
+  } else {
+    if (lc.fp64)
+      row_pass<LOGN, INV, Fp64Arith>(src, dst, lc, op, part, lds);
+    else
+      row_pass<LOGN, INV, IntArith>(src, dst, lc, op, part, lds);
+  }
+}
+
+template <int LOGN>
+static hipError_t launch_split_t(bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
+  using S = Split<LOGN>;
+  const dim3 grid(njobs * S::PARTS), block(64);
+  if (!inverse) {
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false>), grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, true>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
+  switch (logn) {
+    case 13: return launch_split_t<13>(inverse, a, njobs, s);
+    case 14: return launch_split_t<14>(inverse, a, njobs, s);
+    case 15: return launch_split_t<15>(inverse, a, njobs, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace th

@@ -45,8 +45,6 @@ struct NttArgs {
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
-// Dynamic LDS bytes the NTT kernel for 2^logn uses (for occupancy reports).
-size_t ntt_lds_bytes(int logn);
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;

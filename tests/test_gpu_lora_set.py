@@ -85,6 +85,23 @@ def test_lora_set_matches_oracle(env, rescale):
     assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=rescale), got_sums)
 
 
+def test_lora_set_full_token_shape(env):
+    """28 layers x {q, v} (224 products: the launches take the split-NTT path); layers 0 and 27
+    against the oracle, and the device-resident run equal to the host-I/O run."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(14)
+    H = rng.normal(size=(28, 1536)) * 0.1
+    proj = [(l, rng.normal(size=(16, 1536)) * 0.02, rng.normal(size=(o, 16)) * 0.02)
+            for l in range(28) for o in (1536, 256)]
+    ls = zero_moai.LoraSet(eng, 28, proj)
+    seeds = list(range(100, 128))
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    for l in (0, 27):
+        sub = proj[2 * l:2 * l + 2]
+        exp, exp_sums = _oracle(ref, rpk, rsk, H[l:l + 1], seeds[l:l + 1], [(0, A, B) for _, A, B in sub], True)
+        _check(got[2 * l:2 * l + 2], got_sums[8 * l:8 * l + 8], exp, exp_sums)
+
+
 def test_lora_set_ragged_shapes(env):
     """Ranks that do not fill the last batch, d with cols = 8, uneven d_out, inputs shared unevenly."""
     eng, ref, sk, pk, rsk, rpk = env

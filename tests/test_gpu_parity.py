@@ -76,6 +76,26 @@ def test_ntt_default_chains(n):
     assert np.array_equal(ctx.ntt_inverse(fwd), x)
 
 
+@pytest.mark.parametrize("n,polys", [(8192, 72), (16384, 72)])
+def test_ntt_large_batch_matches_oracle(n, polys):
+    """More than 256 transforms per launch: the column + row pass kernels."""
+    q = orc.default_chain(n)
+    ctx = tensafe_he.CkksContext(n)
+    rng = np.random.default_rng(n + polys)
+    x = np.stack([rng.integers(0, qq, (polys, n), dtype=np.uint64) for qq in q], axis=1)
+    x[5, :, :7] = 0
+    x[6, :, -7:] = np.array(q, np.uint64)[:, None] - 1
+    fwd = ctx.ntt_forward(x)
+    for p in (0, 5, 6, polys - 1):
+        for l, qq in enumerate(q):
+            assert np.array_equal(fwd[p, l], orc.ntt_forward(x[p, l], qq)), f"forward poly {p} limb {l}"
+    inv = ctx.ntt_inverse(x)
+    for p in (0, 6, polys - 1):
+        for l, qq in enumerate(q):
+            assert np.array_equal(inv[p, l], orc.ntt_inverse(x[p, l], qq)), f"inverse poly {p} limb {l}"
+    assert np.array_equal(ctx.ntt_inverse(fwd), x)
+
+
 def test_ntt_batched_microbench_shape(eng16):
     """64 polynomials x 4 limbs at N=16384 (the batched round-trip workload)."""
     rng = np.random.default_rng(7)
