@@ -61,7 +61,7 @@ int th_device_count(int* count);
 /* Replaces CkksContext::new (lib.rs:35-56, ciphertext.rs:61-74).
  * moduli == NULL selects the reference chain for N in {8192, 16384, 32768}
  * (params.rs:66-126); otherwise `L` distinct NTT-friendly primes
- * (q = 1 mod 2N, q < 2^62) define the chain. scale_bits must be 40
+ * (q = 1 mod 2N, q < 2^61) define the chain. scale_bits must be 40
  * (params.rs:9). */
 int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale_bits, int device,
                   th_ctx** out);

@@ -1,8 +1,9 @@
 // Butterfly arithmetic and load-side operations shared by the NTT kernels.
 //
 // Two exact modular-multiply policies (chosen per limb prime):
-//  IntArith  - 64-bit Shoup products with Harvey's lazy ranges
-//              ([0, 4q) forward, [0, 2q) inverse); any q < 2^62.
+//  IntArith  - 64-bit Shoup products with an approximate quotient (at most
+//              2 short) and lazy ranges [0, 8q) forward, [0, 4q) inverse;
+//              q < 2^61 so that 8q fits in 64 bits.
 //  Fp64Arith - q < 2^41: exact products from one FMA split and a quotient
 //              rounded from x * (w / q); values are exact integers in doubles.
 // Both end on the canonical residue, so transforms are bit-identical to the
@@ -19,29 +20,30 @@ namespace th {
 struct IntArith {
   using V = uint64_t;
   using Tw = ShoupTw;
-  uint64_t q, two_q;
-  __device__ IntArith(const LimbConst& c) : q(c.q), two_q(c.two_q) {}
+  uint64_t q, two_q, four_q;
+  __device__ IntArith(const LimbConst& c) : q(c.q), two_q(c.two_q), four_q(2 * c.two_q) {}
   __device__ __forceinline__ V load(uint64_t x) const { return x; }
-  // forward CT butterfly, inputs/outputs in [0, 4q)
+  // forward CT butterfly, inputs/outputs in [0, 8q): X < 4q, T < 4q
   __device__ __forceinline__ void fwd(V& a, V& b, const Tw& t) const {
-    uint64_t X = csub(a, two_q);
-    uint64_t T = shoup_lazy(b, t.w, t.ws, q);
+    const uint64_t X = csub(a, four_q);
+    const uint64_t T = shoup_approx(b, t.w, t.ws, q);
     a = X + T;
-    b = X + two_q - T;
+    b = X + four_q - T;
   }
-  // inverse GS butterfly, inputs/outputs in [0, 2q)
+  // inverse GS butterfly, inputs/outputs in [0, 4q)
   __device__ __forceinline__ void inv(V& a, V& b, const Tw& t) const {
-    uint64_t X = a, Y = b;
-    a = csub(X + Y, two_q);
-    b = shoup_lazy(X + two_q - Y, t.w, t.ws, q);
+    const uint64_t X = a, Y = b;
+    a = csub(X + Y, four_q);
+    b = shoup_approx(X + four_q - Y, t.w, t.ws, q);
   }
+  // last inverse stage with N^{-1} folded in; canonical outputs
   __device__ __forceinline__ void inv_last(V& a, V& b, const LimbConst& c) const {
-    uint64_t X = a, Y = b;
-    a = csub(shoup_lazy(X + Y, c.n_inv, c.n_inv_s, q), q);
-    b = csub(shoup_lazy(X + two_q - Y, c.last_w, c.last_ws, q), q);
+    const uint64_t X = a, Y = b;
+    a = csub(csub(shoup_approx(X + Y, c.n_inv, c.n_inv_s, q), two_q), q);
+    b = csub(csub(shoup_approx(X + four_q - Y, c.last_w, c.last_ws, q), two_q), q);
   }
   __device__ __forceinline__ void inv_pass_end(V&) const {}
-  __device__ __forceinline__ uint64_t fwd_store(V x) const { return csub(csub(x, two_q), q); }
+  __device__ __forceinline__ uint64_t fwd_store(V x) const { return csub(csub(csub(x, four_q), two_q), q); }
   __device__ __forceinline__ uint64_t inv_store(V x) const { return x; }
   __device__ __forceinline__ uint64_t raw(V x) const { return x; }
   __device__ __forceinline__ V unraw(uint64_t x) const { return x; }

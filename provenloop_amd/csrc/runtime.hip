@@ -821,7 +821,7 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       need(L >= 1 && L <= 16, "L must be in [1, 16]");
       q.assign(moduli, moduli + L);
       for (uint32_t i = 0; i < L; ++i) {
-        need(q[i] < (1ULL << 62), "moduli must be below 2^62");
+        need(q[i] < (1ULL << 61), "moduli must be below 2^61");
         need(q[i] % (2ULL * N) == 1, "modulus " + std::to_string(q[i]) + " is not 1 mod 2N");
         need(is_prime(q[i]), "modulus " + std::to_string(q[i]) + " is not prime");
         for (uint32_t j = 0; j < i; ++j) need(q[i] != q[j], "moduli must be distinct");

@@ -7,7 +7,7 @@
 //
 // Two exact modular-multiply paths are used, chosen per prime:
 //  * "int":  64-bit Shoup multiply with a precomputed floor(w*2^64/q) and
-//            Harvey lazy reduction (values kept in [0, 4q)); any q < 2^62.
+//            Harvey-style lazy reduction; any q < 2^61.
 //  * "fp64": for q < 2^41 the product w*x is split exactly into hi + lo with
 //            one FMA and the quotient comes from x*(w/q) rounded to nearest;
 //            the remainder is exact (all intermediate integers < 2^53). Six
@@ -52,6 +52,22 @@ __device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t 
 }
 
 __device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t m) { return x >= m ? x - m : x; }
+
+// floor(x * s / 2^64) - e with e in {0, 1, 2}: x1*s1 + hi(x1*s0) + hi(x0*s1)
+// for 32-bit halves; the low halves of the two cross products and hi(x0*s0)
+// are dropped, each below 2^32, so at most 2 is lost after the shift.
+__device__ __forceinline__ uint64_t mulhi_approx(uint64_t x, uint64_t s) {
+  const uint32_t x0 = (uint32_t)x, x1 = (uint32_t)(x >> 32), s0 = (uint32_t)s, s1 = (uint32_t)(s >> 32);
+  const uint64_t h = (uint64_t)__umulhi(x1, s0) + __umulhi(x0, s1);
+  return (uint64_t)x1 * s1 + h;
+}
+
+// x * w mod q in [0, 4q) for any 64-bit x (w < q, ws = floor(w * 2^64 / q)):
+// the exact Shoup remainder is below 2q and the quotient estimate is at most
+// 2 short.
+__device__ __forceinline__ uint64_t shoup_approx(uint64_t x, uint64_t w, uint64_t ws, uint64_t q) {
+  return x * w - mulhi_approx(x, ws) * q;
+}
 
 // Exact a*b mod q for a, b < q < 2^63 (operands without a precomputed
 // companion): 128-bit product, quotient from the high word scaled by a

@@ -74,6 +74,9 @@ def test_c_abi_rejects_bad_context_arguments():
     notfriendly = np.array([1152921504606748673, 1099511627791], np.uint64)
     rc = L.th_ctx_create(16384, _lib.ptr(notfriendly), 2, 40, 0, ctypes.byref(out))
     assert rc == _lib.TH_EINVAL and "not 1 mod 2N" in _lib.last_error()
+    wide = np.array([1152921504606748673, (1 << 61) + 1], np.uint64)  # the lazy NTT ranges need 8q < 2^64
+    rc = L.th_ctx_create(16384, _lib.ptr(wide), 2, 40, 0, ctypes.byref(out))
+    assert rc == _lib.TH_EINVAL and "below 2^61" in _lib.last_error()
     assert not out.value
 
 
