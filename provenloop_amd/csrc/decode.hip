@@ -33,13 +33,11 @@ __device__ __forceinline__ double u128_to_f64(uint64_t hi, uint64_t lo) {
   return ldexp((double)mant, 75 - lz);
 }
 
-// Decrypted coefficient j as the reference's f64 value before the twist.
-__device__ __forceinline__ double coeff_value(const DecodeJob& jb, const DecodeConst& dc, uint32_t j,
-                                              uint32_t n) {
+// Decrypted coefficient j, centred (or CRT-combined and centred), as f64.
+__device__ __forceinline__ double coeff_centred(const DecodeJob& jb, const DecodeConst& dc, uint32_t j, uint32_t n) {
   if (!jb.crt) {
     const uint64_t c = jb.m[j];
-    const double s = c > dc.half_q0 ? -((double)(dc.q0 - c)) : (double)c;
-    return s / jb.scale;
+    return c > dc.half_q0 ? -((double)(dc.q0 - c)) : (double)c;
   }
   // ciphertext.rs:360-392
   const uint64_t m0 = jb.m[j], m1 = jb.m[n + j];
@@ -56,15 +54,18 @@ __device__ __forceinline__ double coeff_value(const DecodeJob& jb, const DecodeC
     hi = hi - dc.Q_hi - (lo < dc.Q_lo ? 1 : 0);
     lo = nlo;
   }
-  double v;
   if (hi > dc.halfQ_hi || (hi == dc.halfQ_hi && lo > dc.halfQ_lo)) {
     const uint64_t dlo = dc.Q_lo - lo;
     const uint64_t dhi = dc.Q_hi - hi - (dc.Q_lo < lo ? 1 : 0);
-    v = -u128_to_f64(dhi, dlo);
-  } else {
-    v = u128_to_f64(hi, lo);
+    return -u128_to_f64(dhi, dlo);
   }
-  return v / jb.scale;
+  return u128_to_f64(hi, lo);
+}
+
+// The reference's f64 coefficient value before the twist (encoding.rs:221-233,
+// ciphertext.rs:360-392): centred value / scale.
+__device__ __forceinline__ double coeff_value(const DecodeJob& jb, const DecodeConst& dc, uint32_t j, uint32_t n) {
+  return coeff_centred(jb, dc, j, n) / jb.scale;
 }
 
 constexpr int DEC_THREADS = 1024;
@@ -156,6 +157,71 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* _
 }
 
 size_t decode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
+
+// ZeRo-MOAI segment sums straight from the decrypted coefficients:
+// seg[c] = (sum_j m_j W[c][j]) / scale with m_j the decode's centred (or
+// CRT-combined) coefficient and W the host-computed segment weights. Equal to
+// decoding and summing the slots up to rounding (the slots themselves are
+// never formed). Each job is cut into SEGSUM_CHUNKS chunks of coefficients,
+// one workgroup each, whose partial sums go to the job's scratch (parts);
+// a second kernel adds them in chunk order, so results are deterministic.
+constexpr uint32_t SEGSUM_CHUNKS = 16;
+
+template <int MAXC>
+__global__ __launch_bounds__(256) void k_segsum_partial(const DecodeJob* __restrict__ jobs,
+                                                        const DecodeConst* __restrict__ dcp,
+                                                        const double* __restrict__ W, uint32_t n, uint32_t cols) {
+  __shared__ double part[4][MAXC];
+  const DecodeConst dc = *dcp;
+  const DecodeJob jb = jobs[blockIdx.y];
+  const uint32_t len = n / SEGSUM_CHUNKS, base = blockIdx.x * len;
+  double acc[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
+  for (uint32_t j = base + threadIdx.x; j < base + len; j += blockDim.x) {
+    const double v = coeff_centred(jb, dc, j, n);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (c < (int)cols) acc[c] += v * W[(size_t)c * n + j];
+  }
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    double a = acc[c];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
+    if (lane == 0) part[wave][c] = a;
+  }
+  __syncthreads();
+  if (threadIdx.x < cols) {
+    const int c = threadIdx.x;
+    jb.parts[blockIdx.x * cols + c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
+  }
+}
+
+__global__ void k_segsum_final(const DecodeJob* __restrict__ jobs, uint32_t njobs, uint32_t cols) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= njobs * cols) return;
+  const DecodeJob jb = jobs[t / cols];
+  const uint32_t c = t % cols;
+  double s = 0.0;
+  for (uint32_t k = 0; k < SEGSUM_CHUNKS; ++k) s += jb.parts[k * cols + c];
+  jb.seg[c] = s / jb.scale;
+}
+
+hipError_t launch_segsum(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* W,
+                         uint32_t logn, uint32_t cols, hipStream_t s) {
+  if (!njobs) return hipSuccess;
+  if (cols < 1 || cols > SEGSUM_MAX_COLS) return hipErrorInvalidValue;
+  const uint32_t n = 1u << logn;
+  const dim3 grid(SEGSUM_CHUNKS, njobs);
+  if (cols <= 8)
+    hipLaunchKernelGGL(k_segsum_partial<8>, grid, dim3(256), 0, s, jobs, dc, W, n, cols);
+  else
+    hipLaunchKernelGGL(k_segsum_partial<SEGSUM_MAX_COLS>, grid, dim3(256), 0, s, jobs, dc, W, n, cols);
+  hipLaunchKernelGGL(k_segsum_final, dim3((njobs * cols + 255) / 256), dim3(256), 0, s, jobs, njobs, cols);
+  return hipGetLastError();
+}
 
 hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,

@@ -19,12 +19,14 @@ constexpr int ENC_THREADS = 1024;
 template <int LP>
 __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* __restrict__ jobs,
                                                               const double* __restrict__ stage_re,
-                                                              const double* __restrict__ stage_im, uint32_t logn) {
+                                                              const double* __restrict__ stage_im, uint32_t logn,
+                                                              const double* __restrict__ z_base) {
   extern __shared__ double sh[];
   const uint32_t n = 1u << logn, S = n / 2;
   const uint32_t M = n >> LP;
   const uint32_t part = blockIdx.x;
   const EncodeJob jb = jobs[blockIdx.y];
+  const double* z = z_base ? z_base + (size_t)blockIdx.y * (jb.rep_d ? jb.rep_d : S) : jb.z;
   double* re = sh;
   double* im = sh + M;
   const uint32_t r = brv_bits(part, LP);
@@ -35,9 +37,9 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
     const uint32_t slot = j < S ? j : n - 1 - j;
     double v;
     if (jb.rep_d)  // inference_engine.py:1266-1269: [h | h | ... | 0]
-      v = slot < jb.rep_cols * jb.rep_d ? jb.z[slot % jb.rep_d] : 0.0;
+      v = slot < jb.rep_cols * jb.rep_d ? z[slot % jb.rep_d] : 0.0;
     else
-      v = jb.z[slot];
+      v = z[slot];
     re[pos] = v;
     im[pos] = 0.0;
   }
@@ -128,7 +130,7 @@ size_t encode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s) {
+                         uint32_t L, hipStream_t s, const double* z_base) {
   if (!njobs) return hipSuccess;
   const uint32_t lp = fft_parts_log(logn);
   const uint32_t M = (1u << logn) >> lp;
@@ -141,7 +143,7 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
                             (int)lds);                                                                     \
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(ENC_THREADS), lds, s, jobs,         \
-                       stage_re, stage_im, logn);                                                          \
+                       stage_re, stage_im, logn, z_base);                                                  \
     hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im, \
                        stage_re, stage_im, logn, L);                                                       \
     return hipGetLastError();

@@ -15,10 +15,12 @@ struct EncodeJob {
   double* parts;       // scratch, encode_parts_doubles(logn) doubles
 };
 
-// Encode z and write the per-limb residues of m (+ e0), e1 and u.
+// Encode z and write the per-limb residues of m (+ e0), e1 and u. With
+// z_base, job i reads its input at z_base + i * (rep_d, or N/2 without
+// replication) instead of its z field.
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s);
+                         uint32_t L, hipStream_t s, const double* z_base = nullptr);
 size_t encode_parts_doubles(uint32_t logn);
 
 struct SampleJob {
@@ -30,7 +32,10 @@ struct SampleJob {
 
 // encrypt_pk's randomness (ciphertext.rs:255-273) for each job, drawn from the
 // job's ChaCha20 stream in the reference's order. force_serial makes every job
-// take the serial path that handles range_u32 rejections (for testing).
-hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s);
+// take the serial path that handles range_u32 rejections (for testing). With
+// seeds (host array, one per job) the jobs' seed fields are ignored and the
+// seeds travel in the launch arguments.
+hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
+                            const uint64_t* seeds = nullptr);
 
 }  // namespace th

@@ -7,6 +7,8 @@
 #include "host_math.h"
 
 #include <math.h>
+
+#include <algorithm>
 #include <stdio.h>
 #include <string.h>
 
@@ -204,6 +206,31 @@ void Encoder::init(uint32_t nn) {
     for (uint32_t k = 0; k < half; ++k) {
       double angle = -2.0 * kPi * (double)k / (double)(2 * half);  // encoding.rs:70-74
       sincos(angle, &stage_im[half - 1 + k], &stage_re[half - 1 + k]);
+    }
+  }
+}
+
+}  // namespace th
+
+namespace th {
+
+void segment_weights(uint32_t n, uint32_t d, uint32_t cols, double* out) {
+  const uint32_t S = n / 2;
+  const long double pi = 3.141592653589793238462643383279502884L;
+  // angle pi * m / N for an integer m, reduced modulo 2N exactly
+  auto ang = [&](uint64_t m) { return pi * (long double)(m % (2ull * n)) / (long double)n; };
+  for (uint32_t c = 0; c < cols; ++c) {
+    const uint64_t k0 = (uint64_t)c * d, k1 = std::min<uint64_t>((uint64_t)(c + 1) * d, S);
+    double* w = out + (size_t)c * n;
+    for (uint32_t j = 0; j < n; ++j) {
+      if (k1 <= k0) {
+        w[j] = 0.0;
+      } else if (j == 0) {
+        w[j] = (double)(k1 - k0);
+      } else {
+        const long double num = cosl(ang((uint64_t)j * (k0 + k1))) * sinl(ang((uint64_t)j * (k1 - k0)));
+        w[j] = (double)(num / sinl(ang(j)));
+      }
     }
   }
 }

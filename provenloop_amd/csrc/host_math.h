@@ -52,6 +52,17 @@ void draw_gaussian(ChaChaStream& s, size_t n, int64_t* out);
 
 // f64 tables of the canonical-embedding FFT (tensafe-he-core/src/encoding.rs:39-80),
 // uploaded once per context for the GPU encoder and decoder.
+// Weights of the ZeRo-MOAI segment sums taken straight from decrypted
+// coefficients. Decoding (encoding.rs:219-239, :282-315) maps coefficient
+// values v_j (centred, divided by the scale) to slots
+//   z_k = Re(sum_j v_j e^{-i pi j / N} e^{-2 pi i j k / N}),  k < N/2,
+// so the sum of slots [k0, k1) is sum_j v_j W[j] with
+//   W[j] = sum_{k0 <= k < k1} cos(pi j (2k + 1) / N)
+//        = cos(t (k0 + k1)) sin(t (k1 - k0)) / sin t,   t = pi j / N  (W[0] = k1 - k0).
+// out[c * N + j] for segment c = slots [c d, min((c + 1) d, N/2)); long
+// double evaluation with exact integer reduction of the angles.
+void segment_weights(uint32_t n, uint32_t d, uint32_t cols, double* out);
+
 struct Encoder {
   uint32_t n = 0, logn = 0;
   std::vector<double> twist_re, twist_im;   // cos/sin(pi j / N)

@@ -62,8 +62,12 @@ __global__ void k_sub_product(const uint64_t* __restrict__ x, const uint64_t* __
 
 // c0 = b*U + M, c1 = a*U + E1 in the NTT domain (ciphertext.rs:298-312).
 __global__ void k_encrypt_combine(const EncCombineJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
-                                  uint32_t n, uint32_t L) {
-  const EncCombineJob jb = jobs[blockIdx.y];
+                                  uint32_t n, uint32_t L, const uint64_t* __restrict__ pk) {
+  EncCombineJob jb = jobs[blockIdx.y];
+  if (pk) {
+    jb.pk_b = pk;
+    jb.pk_a = pk + (size_t)L * n;
+  }
   const uint32_t total = L * n;
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
     const uint32_t l = e / n;
@@ -97,9 +101,9 @@ hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_lim
 }
 
 hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
-                                  uint32_t n, uint32_t L, hipStream_t s) {
+                                  uint32_t n, uint32_t L, hipStream_t s, const uint64_t* pk) {
   if (!njobs) return hipSuccess;
-  hipLaunchKernelGGL(k_encrypt_combine, grid_for(L * n, njobs), dim3(256), 0, s, jobs, bc, n, L);
+  hipLaunchKernelGGL(k_encrypt_combine, grid_for(L * n, njobs), dim3(256), 0, s, jobs, bc, n, L, pk);
   return hipGetLastError();
 }
 

@@ -65,8 +65,9 @@ hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_li
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
                             uint32_t n, hipStream_t s);
+// pk (optional): the public key [b | a] for every job instead of the jobs' fields.
 hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
-                                  uint32_t n, uint32_t L, hipStream_t s);
+                                  uint32_t n, uint32_t L, hipStream_t s, const uint64_t* pk = nullptr);
 hipError_t launch_signed_to_rns(const int64_t* x, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
                                hipStream_t s);
 hipError_t launch_sub_product(const uint64_t* x, const uint64_t* a, const uint64_t* sk, uint64_t* out,
@@ -78,5 +79,12 @@ hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeCons
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t d, uint32_t cols, hipStream_t s);
 size_t decode_parts_doubles(uint32_t logn);  // scratch doubles per job
+// Segment sums of the decoded slots taken straight from the decrypted
+// coefficients with segment weights W (cols x N, segment_weights()); each
+// job's `seg` receives cols sums, within rounding of decode-then-sum. Uses
+// the first 16 * cols doubles of each job's `parts` as scratch.
+constexpr uint32_t SEGSUM_MAX_COLS = 16;
+hipError_t launch_segsum(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* W,
+                         uint32_t logn, uint32_t cols, hipStream_t s);
 
 }  // namespace th

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <new>
 #include <stdexcept>
@@ -169,6 +170,7 @@ struct th_ctx {
   int force_serial = 0;   // TH_OPT_FORCE_SERIAL_SAMPLER
   DevicePool pool;
   StagingRing ring;
+  std::map<std::pair<uint32_t, uint32_t>, double*> seg_w;  // segment-sum weights by (d, cols)
   std::mutex mu;
 };
 
@@ -211,14 +213,15 @@ struct th_lora {
   uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
   double* sums = nullptr;      // n_batches x cols
   double* deltas = nullptr;    // n_deltas
-  SampleJob* d_sample = nullptr;
-  EncCombineJob* d_comb = nullptr;
+  const SampleJob* d_sample = nullptr;
+  const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
   const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr, *d_dot_n = nullptr;
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
   const CtPtJob* d_ctpt = nullptr;
   const LoraBJob* d_bjobs = nullptr;
   uint32_t dot_n_jobs = 0, dot_r_jobs = 0;
+  const double* seg_w = nullptr;  // segment weights, or null: decode the slots and sum them
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
     owned.push_back(p);
@@ -450,6 +453,7 @@ void destroy_ctx(th_ctx* c) {
                   c->d_stage_re, c->d_stage_im, c->d_tables};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
+  for (auto& kv : c->seg_w) (void)hipFree(kv.second);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -596,9 +600,26 @@ std::vector<CtView> views_of(const th_ct* const* cts, size_t count) {
   return v;
 }
 
+// Segment-sum weights for (d, cols), built on first use and kept for the
+// context's lifetime (cols x N doubles).
+const double* seg_weights(th_ctx* c, uint32_t d, uint32_t cols) {
+  auto key = std::make_pair(d, cols);
+  auto it = c->seg_w.find(key);
+  if (it != c->seg_w.end()) return it->second;
+  std::vector<double> w((size_t)cols * c->N);
+  segment_weights(c->N, d, cols, w.data());
+  double* dev = nullptr;
+  HIPCHK(hipMalloc(&dev, w.size() * 8));
+  c->seg_w[key] = dev;
+  HIPCHK(hipMemcpy(dev, w.data(), w.size() * 8, hipMemcpyHostToDevice));
+  return dev;
+}
+
 // Queue decrypt + decode of the views; slots to out_dev (count x S) and/or
 // segment sums to seg_dev (count x cols). m_l = c0_l + c1_l * s_l
 // (ciphertext.rs:332-341) is formed inside the inverse transform's load.
+// When only segment sums are wanted (and cols <= SEGSUM_MAX_COLS) they come
+// from the coefficients and the segment weights, without forming the slots.
 // Scratch lives in the caller's scope.
 void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk, double* out_dev, double* seg_dev,
                    uint32_t d, uint32_t cols) {
@@ -624,8 +645,11 @@ void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk,
     dec[i].crt = nl == 2;
   }
   ntt_list(sc, true, nj, NTT_LOAD_DOT, nullptr, sk->d);
-  HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
-                       c->d_stage_im, c->logn, d, cols, c->stream));
+  if (seg_dev && !out_dev && cols <= SEGSUM_MAX_COLS)
+    HIPCHK(launch_segsum(sc.up(dec), (uint32_t)count, c->d_dc, seg_weights(c, d, cols), c->logn, cols, c->stream));
+  else
+    HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
+                         c->d_stage_im, c->logn, d, cols, c->stream));
 }
 
 // out[i] = in[i] x pt[i] on in[i]'s limbs (ciphertext.rs:422-429); out[i] has 2 x limbs limb-polys.
@@ -1380,8 +1404,17 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   double* dec_parts = (double*)set->alloc(nb * decode_parts_doubles(c->logn) * 8);
   set->sums = (double*)set->alloc((size_t)nb * cols * 8);
   set->deltas = (double*)set->alloc(set->n_deltas * 8);
-  set->d_sample = (SampleJob*)set->alloc(ni * sizeof(SampleJob));
-  set->d_comb = (EncCombineJob*)set->alloc(ni * sizeof(EncCombineJob));
+  {
+    // sampler and combine jobs; seeds and the public key come with each launch
+    std::vector<SampleJob> sj(ni);
+    std::vector<EncCombineJob> cj(ni);
+    for (uint32_t i = 0; i < ni; ++i) {
+      sj[i] = SampleJob{0, set->u + (size_t)i * N, set->e0 + (size_t)i * N, set->e1 + (size_t)i * N};
+      cj[i] = EncCombineJob{set->prep + (size_t)i * 3 * L * N, nullptr, nullptr, set->cts + (size_t)i * 2 * L * N};
+    }
+    set->d_sample = persist(set, sj);
+    set->d_comb = persist(set, cj);
+  }
   // encode the plaintext batches (th_encode_to_ntt of each packed vector)
   {
     OpScope sc(c);
@@ -1444,6 +1477,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->d_dec_n = persist(set, dec_n);
   set->d_ctpt = persist(set, cp);
   set->d_bjobs = persist(set, bj);
+  if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
   HIPCHK(hipStreamSynchronize(c->stream));
 }
 
@@ -1518,46 +1552,35 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     need(!do_rescale || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
     const size_t hbytes = (size_t)ni * set->d * 8;
     hipStream_t st = ctx->stream;
-    if (hidden_on_device) {
-      HIPCHK(hipMemcpyAsync(set->hidden, hidden, hbytes, hipMemcpyDeviceToDevice, st));
-    } else {
+    // device-resident inputs are read where they are; host inputs go through one copy
+    const double* z = hidden;
+    if (!hidden_on_device) {
       void* h = ctx->ring.reserve(hbytes, st);
       memcpy(h, hidden, hbytes);
       HIPCHK(hipMemcpyAsync(set->hidden, h, hbytes, hipMemcpyHostToDevice, st));
+      z = set->hidden;
     }
-    // per-call jobs: the seeds and the public key
-    std::vector<SampleJob> sj(ni);
-    std::vector<EncCombineJob> cj(ni);
-    for (uint32_t i = 0; i < ni; ++i) {
-      sj[i] = SampleJob{seeds[i], set->u + (size_t)i * N, set->e0 + (size_t)i * N, set->e1 + (size_t)i * N};
-      cj[i] = EncCombineJob{set->prep + (size_t)i * 3 * L * N, pk->d, pk->d + (size_t)L * N,
-                            set->cts + (size_t)i * 2 * L * N};
-    }
-    const size_t sjb = ni * sizeof(SampleJob), cjb = ni * sizeof(EncCombineJob);
-    void* h = ctx->ring.reserve(sjb + cjb, st);
-    memcpy(h, sj.data(), sjb);
-    memcpy((char*)h + sjb, cj.data(), cjb);
-    HIPCHK(hipMemcpyAsync(set->d_sample, h, sjb, hipMemcpyHostToDevice, st));
-    HIPCHK(hipMemcpyAsync(set->d_comb, (char*)h + sjb, cjb, hipMemcpyHostToDevice, st));
-    // encrypt_pk of every input (ciphertext.rs:240-319)
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st));
+    // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds));
     HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                         ctx->d_stage_im, ctx->logn, L, st));
+                         ctx->d_stage_im, ctx->logn, L, st, z));
     ntt_strided(ctx, false, set->prep, set->prep, ni * 3 * L, L);
-    HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st));
+    HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
     if (do_rescale) {
       // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
       launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2 * L, NTT_LOAD_MUL);
       launch_jobs_ntt(ctx, false, set->d_fwd_rs, nb * 2 * (L - 1), NTT_LOAD_RESCALE, ctx->d_rc + (size_t)L * L);
       launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
-      HIPCHK(launch_decode(set->d_dec_r, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
     } else {
       HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
       launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
-      HIPCHK(launch_decode(set->d_dec_n, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
     }
+    const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
+    if (set->seg_w)
+      HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));
+    else
+      HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
     double* dout = deltas_on_device ? deltas : set->deltas;
     HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
     const size_t db = set->n_deltas * 8, ib = (size_t)nb * set->cols * 8;

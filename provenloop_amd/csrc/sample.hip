@@ -65,14 +65,26 @@ __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t w1, ui
   return (int64_t)r;
 }
 
+// Seeds of up to SEEDS_PER_LAUNCH jobs passed with the launch itself, so a
+// caller whose job arrays stay in device memory needs no copy per call.
+constexpr uint32_t SEEDS_PER_LAUNCH = 64;
+struct SeedBlock {
+  uint64_t v[SEEDS_PER_LAUNCH];
+};
+
+__device__ __forceinline__ uint64_t job_seed(const SampleJob& jb, const SeedBlock& sb, int use_sb, uint32_t j) {
+  return use_sb ? sb.v[j] : jb.seed;
+}
+
 // One thread per 16-word block of the stream.
-__global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n) {
+__global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, SeedBlock sb, int use_sb) {
   const SampleJob jb = jobs[blockIdx.y];
+  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.y);
   const uint32_t nblocks = 9 * (n / 16);
   const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= nblocks) return;
   uint32_t w[16];
-  chacha20((uint32_t)jb.seed, (uint32_t)(jb.seed >> 32), b, w);
+  chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
   if (b < n / 16) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) jb.u[16 * b + i] = ternary_value(w[i]);
@@ -106,18 +118,20 @@ struct SerialStream {
 
 // One workgroup per job: re-derive the u words; if any was rejected (== 0),
 // or force_serial is set, lane 0 rewrites u, e0 and e1 by the serial walk.
-__global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restrict__ jobs, uint32_t n, int force_serial) {
+__global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restrict__ jobs, uint32_t n, int force_serial,
+                                                      SeedBlock sb, int use_sb) {
   const SampleJob jb = jobs[blockIdx.x];
+  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.x);
   int bad = 0;
   for (uint32_t b = threadIdx.x; b < n / 16; b += blockDim.x) {
     uint32_t w[16];
-    chacha20((uint32_t)jb.seed, (uint32_t)(jb.seed >> 32), b, w);
+    chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
 #pragma unroll
     for (int i = 0; i < 16; ++i) bad |= (w[i] == 0);
   }
   bad = __syncthreads_or(bad) | force_serial;
   if (!bad || threadIdx.x != 0) return;
-  SerialStream st(jb.seed);
+  SerialStream st(seed);
   for (uint32_t i = 0; i < n; ++i) {
     uint32_t r = st.next();
     for (uint32_t guard = 0; r < 1 && guard < (1u << 20); ++guard) r = st.next();  // rng.rs:112-119
@@ -133,12 +147,21 @@ __global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restric
   }
 }
 
-hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s) {
+hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
+                            const uint64_t* seeds) {
   if (!njobs) return hipSuccess;
   if (n % 16) return hipErrorInvalidValue;
   const uint32_t nblocks = 9 * (n / 16);
-  hipLaunchKernelGGL(k_sample_blocks, dim3((nblocks + 255) / 256, njobs), dim3(256), 0, s, jobs, n);
-  hipLaunchKernelGGL(k_sample_check, dim3(njobs), dim3(256), 0, s, jobs, n, force_serial);
+  SeedBlock sb{};
+  for (uint32_t first = 0; first < njobs; first += SEEDS_PER_LAUNCH) {
+    const uint32_t cnt = njobs - first < SEEDS_PER_LAUNCH ? njobs - first : SEEDS_PER_LAUNCH;
+    if (seeds)
+      for (uint32_t i = 0; i < cnt; ++i) sb.v[i] = seeds[first + i];
+    hipLaunchKernelGGL(k_sample_blocks, dim3((nblocks + 255) / 256, cnt), dim3(256), 0, s, jobs + first, n, sb,
+                       seeds != nullptr);
+    hipLaunchKernelGGL(k_sample_check, dim3(cnt), dim3(256), 0, s, jobs + first, n, force_serial, sb,
+                       seeds != nullptr);
+  }
   return hipGetLastError();
 }
 
