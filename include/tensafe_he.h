@@ -209,8 +209,11 @@ int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, ui
  *   deltas: n_deltas doubles (projection j at offset sum_{k<j} d_out[k]),
  *           device memory if deltas_on_device, else host.
  *   inter:  NULL, or a host array of n_batches x cols segment sums.
- * The call returns after ONE synchronisation of the context stream (plus one
- * device-to-host copy if an output is on the host). */
+ * With hidden and deltas in device memory and inter == NULL the call only
+ * queues the token's kernels on the context stream and returns (no host
+ * synchronisation; order later work with th_ctx_stream / th_ctx_sync).
+ * Otherwise it returns after one synchronisation of the stream and one
+ * device-to-host copy. */
 int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
                    int hidden_on_device, const uint64_t* seeds, int do_rescale, double* deltas,
                    int deltas_on_device, double* inter);

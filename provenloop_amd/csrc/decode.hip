@@ -94,7 +94,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_parts(const DecodeJob* _
     im[pos] = -c * twist_im[j];
   }
   __syncthreads();
-  dit_stages_lds(re, im, lb, stage_re, stage_im);
+  dit_stages_reg(re, im, lb, stage_re, stage_im);
   double* out = jb.parts + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[i];

@@ -44,7 +44,7 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
     im[pos] = 0.0;
   }
   __syncthreads();
-  dit_stages_lds(re, im, lb, stage_re, stage_im);
+  dit_stages_reg(re, im, lb, stage_re, stage_im);
   double* out = jb.parts + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[i];

@@ -24,18 +24,21 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
 size_t encode_parts_doubles(uint32_t logn);
 
 struct SampleJob {
-  uint64_t seed;  // TenSafeRng::from_seed(seed)
-  uint8_t* u;     // n ternary values
-  int64_t* e0;    // n rounded Gaussians
-  int64_t* e1;    // n rounded Gaussians
+  uint64_t seed;     // TenSafeRng::from_seed(seed)
+  uint8_t* u;        // n ternary values
+  int64_t* e0;       // n rounded Gaussians
+  int64_t* e1;       // n rounded Gaussians
+  uint32_t* reject;  // zero-initialised flag set when a u word is rejected, or null
 };
 
 // encrypt_pk's randomness (ciphertext.rs:255-273) for each job, drawn from the
 // job's ChaCha20 stream in the reference's order. force_serial makes every job
 // take the serial path that handles range_u32 rejections (for testing). With
 // seeds (host array, one per job) the jobs' seed fields are ignored and the
-// seeds travel in the launch arguments.
+// seeds travel in the launch arguments. Jobs with a reject flag (all or none
+// of them) skip the re-derivation pass: the block kernel raises the flag and
+// only flagged jobs are replayed; the flag is cleared again.
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
-                            const uint64_t* seeds = nullptr);
+                            const uint64_t* seeds = nullptr, bool flagged = false);
 
 }  // namespace th

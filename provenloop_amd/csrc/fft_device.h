@@ -57,6 +57,52 @@ __device__ __forceinline__ void dit_stages_lds(double* re, double* im, uint32_t 
   }
 }
 
+// The same stages 0 .. lb-1, up to three at a time in registers: for a pass
+// on bits [s0, s0 + R) each thread loads the 2^R values whose positions
+// differ only in those bits, runs the R stages on them and writes them back,
+// so LDS is read and written once per pass instead of once per stage. Every
+// butterfly sees the same operands and twiddle as in dit_stages_lds, so the
+// result is bit-identical. Needs blockDim.x * 8 >= M.
+__device__ __forceinline__ void dit_stages_reg(double* re, double* im, uint32_t lb,
+                                               const double* __restrict__ stage_re,
+                                               const double* __restrict__ stage_im) {
+  const uint32_t M = 1u << lb;
+  for (uint32_t s0 = 0; s0 < lb; s0 += 3) {
+    const uint32_t R = lb - s0 < 3 ? lb - s0 : 3;
+    const uint32_t groups = M >> R;
+    for (uint32_t t = threadIdx.x; t < groups; t += blockDim.x) {
+      const uint32_t lo = t & ((1u << s0) - 1), hi = t >> s0;
+      const uint32_t base = lo | (hi << (s0 + R));
+      Cx x[8];
+#pragma unroll
+      for (uint32_t r = 0; r < 8; ++r)
+        if (r < (1u << R)) x[r] = Cx{re[base | (r << s0)], im[base | (r << s0)]};
+#pragma unroll
+      for (uint32_t rb = 0; rb < 3; ++rb) {
+        if (rb >= R) break;
+        const uint32_t s = s0 + rb, half = 1u << s;
+#pragma unroll
+        for (uint32_t r = 0; r < 8; ++r) {
+          if (r >= (1u << R) || (r & (1u << rb))) continue;
+          // position of x[r] is base | (r << s0); its bits below s select the twiddle
+          const uint32_t k = (base | (r << s0)) & (half - 1);
+          Cx t0, t1;
+          dit(x[r], x[r | (1u << rb)], stage_re[half - 1 + k], stage_im[half - 1 + k], t0, t1);
+          x[r] = t0;
+          x[r | (1u << rb)] = t1;
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < 8; ++r)
+        if (r < (1u << R)) {
+          re[base | (r << s0)] = x[r].re;
+          im[base | (r << s0)] = x[r].im;
+        }
+    }
+    __syncthreads();
+  }
+}
+
 // Parts per transform: one part fits LDS (2^13 complex = 128 KiB).
 __host__ __device__ constexpr uint32_t fft_parts_log(uint32_t logn) { return logn <= 13 ? 0 : logn - 13; }
 

@@ -510,7 +510,7 @@ void queue_encrypt_pk(OpScope& sc, const th_pk* pk, const double* z, size_t coun
   int64_t* e0 = (int64_t*)sc.dev(count * N * 8);
   int64_t* e1 = (int64_t*)sc.dev(count * N * 8);
   std::vector<SampleJob> sj(count);
-  for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], u + i * N, e0 + i * N, e1 + i * N};
+  for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], u + i * N, e0 + i * N, e1 + i * N, nullptr};
   HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
   uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
   queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N, rep_d, rep_cols);
@@ -536,7 +536,7 @@ void encrypt_pk_many(th_ctx* c, const th_pk* pk, const double* zh, size_t count,
     int64_t* de0 = (int64_t*)sc.dev(count * N * 8);
     int64_t* de1 = (int64_t*)sc.dev(count * N * 8);
     std::vector<SampleJob> sj(count);
-    for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], du + i * N, de0 + i * N, de1 + i * N};
+    for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], du + i * N, de0 + i * N, de1 + i * N, nullptr};
     HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
     u = du;
     e0 = de0;
@@ -1408,8 +1408,9 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     // sampler and combine jobs; seeds and the public key come with each launch
     std::vector<SampleJob> sj(ni);
     std::vector<EncCombineJob> cj(ni);
+    uint32_t* reject = const_cast<uint32_t*>(persist(set, std::vector<uint32_t>(ni, 0)));
     for (uint32_t i = 0; i < ni; ++i) {
-      sj[i] = SampleJob{0, set->u + (size_t)i * N, set->e0 + (size_t)i * N, set->e1 + (size_t)i * N};
+      sj[i] = SampleJob{0, set->u + (size_t)i * N, set->e0 + (size_t)i * N, set->e1 + (size_t)i * N, reject + i};
       cj[i] = EncCombineJob{set->prep + (size_t)i * 3 * L * N, nullptr, nullptr, set->cts + (size_t)i * 2 * L * N};
     }
     set->d_sample = persist(set, sj);
@@ -1561,7 +1562,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       z = set->hidden;
     }
     // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds));
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true));
     HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
                          ctx->d_stage_im, ctx->logn, L, st, z));
     ntt_strided(ctx, false, set->prep, set->prep, ni * 3 * L, L);
@@ -1591,7 +1592,8 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       HIPCHK(hipStreamSynchronize(st));
       if (!deltas_on_device) memcpy(deltas, hh, db);
       if (inter) memcpy(inter, hh + db, ib);
-    } else {
+    } else if (!hidden_on_device) {
+      // the host input sits in the staging ring: finish reading it before returning
       HIPCHK(hipStreamSynchronize(st));
     }
   });

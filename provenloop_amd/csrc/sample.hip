@@ -86,8 +86,13 @@ __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, 
   uint32_t w[16];
   chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
   if (b < n / 16) {
+    bool zero = false;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) jb.u[16 * b + i] = ternary_value(w[i]);
+    for (int i = 0; i < 16; ++i) {
+      jb.u[16 * b + i] = ternary_value(w[i]);
+      zero |= w[i] == 0;
+    }
+    if (zero && jb.reject) atomicOr(jb.reject, 1u);  // range_u32 rejects 0 (rng.rs:112-119)
   } else {
     const uint32_t g0 = (16 * b - n) / 4;
 #pragma unroll
@@ -116,21 +121,9 @@ struct SerialStream {
   }
 };
 
-// One workgroup per job: re-derive the u words; if any was rejected (== 0),
-// or force_serial is set, lane 0 rewrites u, e0 and e1 by the serial walk.
-__global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restrict__ jobs, uint32_t n, int force_serial,
-                                                      SeedBlock sb, int use_sb) {
-  const SampleJob jb = jobs[blockIdx.x];
-  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.x);
-  int bad = 0;
-  for (uint32_t b = threadIdx.x; b < n / 16; b += blockDim.x) {
-    uint32_t w[16];
-    chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) bad |= (w[i] == 0);
-  }
-  bad = __syncthreads_or(bad) | force_serial;
-  if (!bad || threadIdx.x != 0) return;
+// The reference's consumption order for one stream, walked serially
+// (handles range_u32 rejections: rng.rs:109-133, ciphertext.rs:255-273).
+__device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_t n) {
   SerialStream st(seed);
   for (uint32_t i = 0; i < n; ++i) {
     uint32_t r = st.next();
@@ -147,8 +140,37 @@ __global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restric
   }
 }
 
+// One workgroup per job: re-derive the u words; if any was rejected (== 0),
+// or force_serial is set, lane 0 rewrites u, e0 and e1 by the serial walk.
+__global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restrict__ jobs, uint32_t n, int force_serial,
+                                                      SeedBlock sb, int use_sb) {
+  const SampleJob jb = jobs[blockIdx.x];
+  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.x);
+  int bad = 0;
+  for (uint32_t b = threadIdx.x; b < n / 16; b += blockDim.x) {
+    uint32_t w[16];
+    chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bad |= (w[i] == 0);
+  }
+  bad = __syncthreads_or(bad) | force_serial;
+  if (!bad || threadIdx.x != 0) return;
+  serial_replay(jb, seed, n);
+}
+
+// One thread per job with a reject flag: replay flagged (or forced) jobs
+// serially, then clear the flag for the next launch.
+__global__ void k_sample_fix(const SampleJob* __restrict__ jobs, uint32_t njobs, uint32_t n, int force_serial,
+                             SeedBlock sb, int use_sb) {
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= njobs) return;
+  const SampleJob jb = jobs[j];
+  if (*jb.reject || force_serial) serial_replay(jb, job_seed(jb, sb, use_sb, j), n);
+  *jb.reject = 0;
+}
+
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
-                            const uint64_t* seeds) {
+                            const uint64_t* seeds, bool flagged) {
   if (!njobs) return hipSuccess;
   if (n % 16) return hipErrorInvalidValue;
   const uint32_t nblocks = 9 * (n / 16);
@@ -159,8 +181,12 @@ hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, i
       for (uint32_t i = 0; i < cnt; ++i) sb.v[i] = seeds[first + i];
     hipLaunchKernelGGL(k_sample_blocks, dim3((nblocks + 255) / 256, cnt), dim3(256), 0, s, jobs + first, n, sb,
                        seeds != nullptr);
-    hipLaunchKernelGGL(k_sample_check, dim3(cnt), dim3(256), 0, s, jobs + first, n, force_serial, sb,
-                       seeds != nullptr);
+    if (flagged)
+      hipLaunchKernelGGL(k_sample_fix, dim3((cnt + 63) / 64), dim3(64), 0, s, jobs + first, cnt, n, force_serial, sb,
+                         seeds != nullptr);
+    else
+      hipLaunchKernelGGL(k_sample_check, dim3(cnt), dim3(256), 0, s, jobs + first, n, force_serial, sb,
+                         seeds != nullptr);
   }
   return hipGetLastError();
 }

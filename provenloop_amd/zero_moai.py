@@ -190,7 +190,9 @@ class LoraSet:
     def deltas_device(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden_dev: int, seeds, dev_out: int,
                       rescale: bool = True):
         """Device in, device out: hidden_dev points at n_inputs x d doubles in
-        HBM, dev_out receives n_deltas doubles; one stream synchronisation."""
+        HBM, dev_out receives n_deltas doubles. Only queues the token on the
+        context stream (no host synchronisation): call ctx.sync(), or order
+        later work after ctx's stream, before reading dev_out."""
         sd = np.ascontiguousarray(seeds, np.uint64)
         if sd.shape != (self.n_inputs,):
             raise ValueError("need one seed per input")

@@ -211,3 +211,21 @@ def test_lora_set_crt_branch_after_rescale():
     got, got_sums = ls.deltas(pk, sk, H, [21], with_intermediates=True)
     exp, exp_sums = _oracle(ref, rpk, rsk, H, [21], proj, True)
     _check(got, got_sums, exp, exp_sums)
+
+
+def test_lora_set_serial_sampler_path(env):
+    """Forcing every input through the serial replay (the path a rejected range_u32 word
+    takes) gives the same deltas, and the per-input reject flags are cleared afterwards."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(15)
+    H = rng.normal(size=(3, 1536)) * 0.1
+    proj = _projections(rng, 3, 1536, ranks=[16, 16, 16], d_outs=[40, 40, 40])
+    ls = zero_moai.LoraSet(eng, 3, proj)
+    base = np.concatenate(ls.deltas(pk, sk, H, [7, 8, 9]))
+    eng._force_serial_sampler(True)
+    try:
+        forced = np.concatenate(ls.deltas(pk, sk, H, [7, 8, 9]))
+    finally:
+        eng._force_serial_sampler(False)
+    again = np.concatenate(ls.deltas(pk, sk, H, [7, 8, 9]))
+    assert np.array_equal(base, forced) and np.array_equal(base, again)
