@@ -148,7 +148,7 @@ __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], t
 
 template <int LOGN, bool INV, class A>
 __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                        const LimbConst& lc, const LoadOp& op, void* lds_raw) {
+                                        const LimbConst& lc, const LoadOp& op, const StoreOp& so, void* lds_raw) {
   using S = Shape<LOGN>;
   const uint32_t tid = threadIdx.x;
   const A ar(lc);
@@ -160,7 +160,7 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
     fwd_passes<LOGN, LOGN, S::COAL_LO, true, A>(x, lds, tid, tw, ar);
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) dst[tid + k * S::T] = ar.fwd_store(x[k]);
+    for (int k = 0; k < S::E; ++k) dst[tid + k * S::T] = so(ar.fwd_store(x[k]), tid + k * S::T);
   } else {
 #pragma unroll
     for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, tid + k * S::T));
@@ -179,27 +179,23 @@ __global__ __launch_bounds__(Shape<LOGN>::T) void ntt_kernel(NttArgs a) {
   uint64_t* dst;
   uint32_t limb;
   LoadOp op{};
+  StoreOp so{};
   if (a.jobs) {
     const NttJob jb = a.jobs[job];
     src = jb.src;
     dst = jb.dst;
     limb = jb.limb;
-    op.kind = a.load;
-    op.aux = jb.aux;
-    if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
-    if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * Shape<LOGN>::N;
-    if (a.load == NTT_LOAD_RESCALE) op.rc = a.rc[limb];
+    job_ops(a, jb, limb, Shape<LOGN>::N, op, so);
   } else {
     src = a.src + (uint64_t)job * a.stride;
     dst = a.dst + (uint64_t)job * a.stride;
     limb = a.limb_base + job % a.limb_mod;
-    op.kind = NTT_LOAD_NONE;
   }
   const LimbConst& lc = a.lc[limb];
   if (lc.fp64)
-    run_ntt<LOGN, INV, Fp64Arith>(src, dst, lc, op, lds);
+    run_ntt<LOGN, INV, Fp64Arith>(src, dst, lc, op, so, lds);
   else
-    run_ntt<LOGN, INV, IntArith>(src, dst, lc, op, lds);
+    run_ntt<LOGN, INV, IntArith>(src, dst, lc, op, so, lds);
 }
 
 template <int LOGN, bool INV>

@@ -94,12 +94,40 @@ struct LoadOp {
     const uint64_t x = src[i];
     switch (kind) {
       case NTT_LOAD_MUL: return mulmod_barrett(x, aux[i], bc);
-      case NTT_LOAD_RESCALE: return rescale_coeff(x, aux[i], rc);
+      case NTT_LOAD_REDUCE: return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
       case NTT_LOAD_DOT: return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
       default: return x;
     }
   }
 };
 
+// The operation fused into a forward transform's final store (NttStore).
+struct StoreOp {
+  uint32_t kind;
+  const uint64_t* aux;
+  const uint64_t* aux2;
+  BarrettConst bc;
+  RescaleConst rc;
+  __device__ __forceinline__ uint64_t operator()(uint64_t y, uint32_t i) const {
+    if (kind == NTT_STORE_NONE) return y;
+    const uint64_t c = kind == NTT_STORE_MUL_RESCALE ? mulmod_barrett(aux[i], aux2[i], bc) : aux[i];
+    return csub(shoup_lazy(submod(c, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
+  }
+};
+
+// Load and store operations of job `jb` in launch `a` for limb `limb`.
+__device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint32_t limb, uint32_t n, LoadOp& op,
+                                        StoreOp& so) {
+  op.kind = a.load;
+  op.aux = jb.aux;
+  if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
+  if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * n;
+  if (a.load == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
+  so.kind = a.store;
+  so.aux = jb.aux;
+  so.aux2 = jb.aux2;
+  if (a.store != NTT_STORE_NONE) so.rc = a.rc[limb];
+  if (a.store == NTT_STORE_MUL_RESCALE) so.bc = a.bc[limb];
+}
 
 }  // namespace th

@@ -153,7 +153,8 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
 // ------------------------------------------------------------------ row pass
 template <int LOGN, bool INV, class A>
 __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                         const LimbConst& lc, const LoadOp& op, uint32_t part, uint64_t* lds_raw) {
+                                         const LimbConst& lc, const LoadOp& op, const StoreOp& so, uint32_t part,
+                                         uint64_t* lds_raw) {
   using S = Split<LOGN>;
   constexpr int CB = S::CB, M = (1 << (CB - 4)) - 1;
   const uint32_t l = threadIdx.x;
@@ -174,7 +175,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
     wave_exchange(x, lds, p2, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) dst[jbase + g(k)] = ar.fwd_store(x[k]);
+    for (int k = 0; k < 16; ++k) dst[jbase + g(k)] = so(ar.fwd_store(x[k]), jbase + g(k));
   } else {
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
 #pragma unroll
@@ -190,8 +191,9 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
 
 // ------------------------------------------------------------------ kernels
 // Workgroup b works on part b % PARTS of job b / PARTS. The pass that reads
-// the transform's input applies the fused load operation; the other pass
-// reads and writes the destination only.
+// the transform's input applies the fused load operation and the forward
+// row pass the fused store operation; otherwise passes read and write the
+// destination only.
 template <int LOGN, bool INV, bool COLUMN>
 __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
@@ -208,21 +210,17 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   uint64_t* dst;
   uint32_t limb;
   LoadOp op{};
+  StoreOp so{};
   if (a.jobs) {
     const NttJob jb = a.jobs[job];
     src = jb.src;
     dst = jb.dst;
     limb = jb.limb;
-    op.kind = a.load;
-    op.aux = jb.aux;
-    if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
-    if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * S::N;
-    if (a.load == NTT_LOAD_RESCALE) op.rc = a.rc[limb];
+    job_ops(a, jb, limb, S::N, op, so);
   } else {
     src = a.src + (uint64_t)job * a.stride;
     dst = a.dst + (uint64_t)job * a.stride;
     limb = a.limb_base + job % a.limb_mod;
-    op.kind = NTT_LOAD_NONE;
   }
   const LimbConst& lc = a.lc[limb];
   if constexpr (COLUMN) {
@@ -232,9 +230,9 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
       column_pass<LOGN, INV, IntArith>(src, dst, lc, op, part, lds);
   } else {
     if (lc.fp64)
-      row_pass<LOGN, INV, Fp64Arith>(src, dst, lc, op, part, lds);
+      row_pass<LOGN, INV, Fp64Arith>(src, dst, lc, op, so, part, lds);
     else
-      row_pass<LOGN, INV, IntArith>(src, dst, lc, op, part, lds);
+      row_pass<LOGN, INV, IntArith>(src, dst, lc, op, so, part, lds);
   }
 }
 

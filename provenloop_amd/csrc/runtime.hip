@@ -319,13 +319,14 @@ void ntt_strided(th_ctx* c, bool inverse, const uint64_t* src, uint64_t* dst, ui
 // the coefficient load (NttLoad): rc is the rescale-constant row of the
 // inputs' level (RESCALE), key the secret key (DOT).
 void ntt_list(OpScope& sc, bool inverse, const std::vector<NttJob>& jobs, NttLoad load = NTT_LOAD_NONE,
-              const RescaleConst* rc = nullptr, const uint64_t* key = nullptr) {
+              const RescaleConst* rc = nullptr, const uint64_t* key = nullptr, NttStore store = NTT_STORE_NONE) {
   th_ctx* c = sc.c;
   if (jobs.empty()) return;
   NttArgs a{};
   a.lc = c->d_lc;
   a.jobs = sc.up(jobs);
   a.load = load;
+  a.store = store;
   a.bc = c->d_bc;
   a.rc = rc;
   a.key = key;
@@ -636,7 +637,7 @@ void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk,
     const uint32_t nl = (ct.scale > kScale * 1.5 && ct.limbs >= 2) ? 2 : 1;
     uint64_t* o = dot + i * 2 * N;
     for (uint32_t l = 0; l < nl; ++l)
-      nj.push_back(NttJob{ct.d + (size_t)l * N, o + (size_t)l * N, ct.d + (size_t)(ct.limbs + l) * N, l, 0});
+      nj.push_back(NttJob{ct.d + (size_t)l * N, o + (size_t)l * N, ct.d + (size_t)(ct.limbs + l) * N, nullptr, l, 0});
     dec[i].m = o;
     dec[i].parts = parts + i * decode_parts_doubles(c->logn);
     dec[i].out = out_dev ? out_dev + i * S : nullptr;
@@ -666,10 +667,13 @@ void queue_ct_pt(OpScope& sc, const std::vector<CtView>& in, const uint64_t* con
 }
 
 // Rescale (ciphertext.rs:476-535) of views that all have L >= 2 limbs into
-// out[i] (2 x (L-1) limb-polys each): inverse NTT of every limb, then a
-// forward NTT of limbs 0..L-2 whose load forms
-// (c_l - (c_last mod q_l)) * (q_last mod q_l)^{-1}. With pts, input i is first
-// multiplied by pts[i] (ct_pt_mul_ntt, ciphertext.rs:422-429) inside the
+// out[i] (2 x (L-1) limb-polys each), in the evaluation domain: for each
+// component, inverse NTT of the last limb only, then for l < L-1 a forward
+// NTT of (c_last mod q_l) whose store forms (C_l - NTT(c_last mod q_l)) *
+// (q_last mod q_l)^{-1}; equal residue for residue to the reference's
+// coefficient-domain rescale because the NTT is linear mod q_l. With pts,
+// input i is first multiplied by pts[i] (ct_pt_mul_ntt, ciphertext.rs:
+// 422-429): C_l = ct_l * pt_l in the store and ct_last * pt_last in the
 // inverse transform's load, so the product ciphertext is never stored.
 void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* out,
                    const uint64_t* const* pts = nullptr) {
@@ -677,24 +681,23 @@ void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* 
   const uint32_t N = c->N;
   const size_t count = in.size();
   const uint32_t L = in[0].limbs;
-  uint64_t* coef = (uint64_t*)sc.dev(count * 2 * L * poly_bytes(c));
-  std::vector<NttJob> inv;
-  inv.reserve(count * 2 * L);
-  for (size_t i = 0; i < count; ++i)
-    for (uint32_t k = 0; k < 2 * L; ++k)
-      inv.push_back(NttJob{in[i].d + (size_t)k * N, coef + (i * 2 * L + k) * N,
-                           pts ? pts[i] + (size_t)(k % L) * N : nullptr, k % L, 0});
-  ntt_list(sc, true, inv, pts ? NTT_LOAD_MUL : NTT_LOAD_NONE);
-  std::vector<NttJob> fwd;
+  uint64_t* last = (uint64_t*)sc.dev(count * 2 * poly_bytes(c));  // coefficient-domain last limbs
+  std::vector<NttJob> inv, fwd;
+  inv.reserve(count * 2);
   fwd.reserve(count * 2 * (L - 1));
   for (size_t i = 0; i < count; ++i)
     for (uint32_t comp = 0; comp < 2; ++comp) {
-      const uint64_t* cc = coef + (i * 2 + comp) * L * N;
+      const uint64_t* cc = in[i].d + (size_t)comp * L * N;
+      uint64_t* lc = last + (i * 2 + comp) * N;
+      inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, pts ? pts[i] + (size_t)(L - 1) * N : nullptr, nullptr,
+                           L - 1, 0});
       for (uint32_t l = 0; l + 1 < L; ++l)
-        fwd.push_back(NttJob{cc + (size_t)l * N, out[i] + (size_t)(comp * (L - 1) + l) * N, cc + (size_t)(L - 1) * N,
-                             l, 0});
+        fwd.push_back(NttJob{lc, out[i] + (size_t)(comp * (L - 1) + l) * N, cc + (size_t)l * N,
+                             pts ? pts[i] + (size_t)l * N : nullptr, l, 0});
     }
-  ntt_list(sc, false, fwd, NTT_LOAD_RESCALE, c->d_rc + (size_t)L * c->L);
+  ntt_list(sc, true, inv, pts ? NTT_LOAD_MUL : NTT_LOAD_NONE);
+  ntt_list(sc, false, fwd, NTT_LOAD_REDUCE, c->d_rc + (size_t)L * c->L, nullptr,
+           pts ? NTT_STORE_MUL_RESCALE : NTT_STORE_RESCALE);
 }
 
 void check_decrypt_args(th_ctx* c, const th_ct* const* cts, size_t count, const th_sk* sk) {
@@ -1344,11 +1347,13 @@ const T* persist(th_lora* set, const std::vector<T>& v) {
 }
 
 void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, NttLoad load,
-                     const RescaleConst* rc = nullptr, const uint64_t* key = nullptr) {
+                     const RescaleConst* rc = nullptr, const uint64_t* key = nullptr,
+                     NttStore store = NTT_STORE_NONE) {
   NttArgs a{};
   a.lc = c->d_lc;
   a.jobs = jobs;
   a.load = load;
+  a.store = store;
   a.bc = c->d_bc;
   a.rc = rc;
   a.key = key;
@@ -1451,23 +1456,29 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     uint64_t* w = set->work + (size_t)bt * 2 * L * N;
     uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
     uint64_t* mm = set->m + (size_t)bt * 2 * N;
-    for (uint32_t k = 0; k < 2 * L; ++k) inv.push_back(NttJob{ct + (size_t)k * N, w + (size_t)k * N, pt + (size_t)(k % L) * N, k % L, 0});
     if (L >= 2) {
-      for (uint32_t comp = 0; comp < 2; ++comp)
+      // evaluation-domain rescale of ct x pt (see queue_rescale): inverse NTT of the product's
+      // last limb (into the batch's work area), forward NTTs of it reduced to each other limb
+      for (uint32_t comp = 0; comp < 2; ++comp) {
+        const uint64_t* cc = ct + (size_t)comp * L * N;
+        uint64_t* lc = w + (size_t)comp * N;
+        inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, pt + (size_t)(L - 1) * N, nullptr, L - 1, 0});
         for (uint32_t l = 0; l + 1 < L; ++l)
-          fwd.push_back(NttJob{w + (size_t)(comp * L + l) * N, r + (size_t)(comp * Lr + l) * N,
-                               w + (size_t)(comp * L + L - 1) * N, l, 0});
-      for (uint32_t l = 0; l < nl_r; ++l) dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(Lr + l) * N, l, 0});
+          fwd.push_back(NttJob{lc, r + (size_t)(comp * Lr + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
+      }
+      for (uint32_t l = 0; l < nl_r; ++l)
+        dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(Lr + l) * N, nullptr, l, 0});
     }
-    for (uint32_t l = 0; l < nl_n; ++l) dot_n.push_back(NttJob{w + (size_t)l * N, mm + (size_t)l * N, w + (size_t)(L + l) * N, l, 0});
+    for (uint32_t l = 0; l < nl_n; ++l)
+      dot_n.push_back(NttJob{w + (size_t)l * N, mm + (size_t)l * N, w + (size_t)(L + l) * N, nullptr, l, 0});
     cp[bt] = CtPtJob{ct, ct + (size_t)L * N, pt, w, L, 0};
     dec_r[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
                           scale_r, nl_r == 2, 0};
     dec_n[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
                           scale_n, nl_n == 2, 0};
   }
-  set->d_inv_mul = persist(set, inv);
   if (L >= 2) {
+    set->d_inv_mul = persist(set, inv);
     set->d_fwd_rs = persist(set, fwd);
     set->d_dot_r = persist(set, dot_r);
     set->d_dec_r = persist(set, dec_r);
@@ -1569,8 +1580,9 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
     if (do_rescale) {
       // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
-      launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2 * L, NTT_LOAD_MUL);
-      launch_jobs_ntt(ctx, false, set->d_fwd_rs, nb * 2 * (L - 1), NTT_LOAD_RESCALE, ctx->d_rc + (size_t)L * L);
+      launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MUL);
+      launch_jobs_ntt(ctx, false, set->d_fwd_rs, nb * 2 * (L - 1), NTT_LOAD_REDUCE, ctx->d_rc + (size_t)L * L, nullptr,
+                      NTT_STORE_MUL_RESCALE);
       launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
     } else {
       HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));

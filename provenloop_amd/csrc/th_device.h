@@ -104,13 +104,6 @@ struct RescaleConst {
   BarrettConst b;          // remainder of a 64-bit value modulo q_l
 };
 
-// ((x - (last mod q)) mod q) * inv mod q for x < q, any 64-bit last
-// (floor rescale, no centring: ciphertext.rs:505-522).
-__device__ __forceinline__ uint64_t rescale_coeff(uint64_t x, uint64_t last, const RescaleConst& c) {
-  const uint64_t lm = last < c.q ? last : mulmod_barrett(last, 1, c.b);
-  return csub(shoup_lazy(submod(x, lm, c.q), c.inv, c.inv_s, c.q), c.q);
-}
-
 // ---------------------------------------------------------------- fp64 path
 // x*w mod q as an exact integer in about (-q/2, q/2); requires |x| < 2^46, w < q < 2^41.
 __device__ __forceinline__ double mulmod_f64(double x, double w, double wq, double q) {

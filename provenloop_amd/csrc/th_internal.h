@@ -12,18 +12,30 @@ namespace th {
 // of the transform's input; the result is what gets transformed):
 //   NONE     x = src[i]
 //   MUL      x = src[i] * aux[i] mod q                    (ct x pt, ciphertext.rs:422-429)
-//   RESCALE  x = (src[i] - (aux[i] mod q)) * q_last^{-1} mod q, aux = coefficient-domain
-//            last limb of the same component             (rescale, ciphertext.rs:505-522)
+//   REDUCE   x = src[i] mod q for any src[i] < 2^61       (a last-limb coefficient
+//                                                         taken to limb q: rescale)
 //   DOT      x = src[i] + aux[i] * key[i] mod q, src = c0, aux = c1, key = s
 //                                                         (decrypt, ciphertext.rs:332-341)
-enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_RESCALE = 2, NTT_LOAD_DOT = 3 };
+enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_REDUCE = 2, NTT_LOAD_DOT = 3 };
+
+// Operation applied to every output of a FORWARD transform before it is
+// stored (fused consumer), y = the transformed value in [0, q):
+//   NONE         dst[i] = y
+//   RESCALE      dst[i] = (aux[i] - y) * q_last^{-1} mod q
+//   MUL_RESCALE  dst[i] = (aux[i] * aux2[i] - y) * q_last^{-1} mod q
+// With y = NTT_q(c_last mod q) these are the rescale of ciphertext.rs:476-535
+// in the evaluation domain: the NTT is linear mod q, so
+//   NTT_q((c_q - (c_last mod q)) * inv) = (C_q - NTT_q(c_last mod q)) * inv
+// for the limb's evaluation-domain input C_q (aux, or the product aux * aux2).
+enum NttStore : uint32_t { NTT_STORE_NONE = 0, NTT_STORE_RESCALE = 1, NTT_STORE_MUL_RESCALE = 2 };
 
 // One limb-polynomial transform. In strided mode job i reads src + i*stride,
 // writes dst + i*stride and uses limb limb_base + i % limb_mod.
 struct NttJob {
   const uint64_t* src;
   uint64_t* dst;
-  const uint64_t* aux;  // second operand of the load operation (null for NONE)
+  const uint64_t* aux;   // operand of the load or store operation
+  const uint64_t* aux2;  // second store operand (MUL_RESCALE)
   uint32_t limb;
   uint32_t pad_;
 };
@@ -37,9 +49,9 @@ struct NttArgs {
   uint32_t limb_mod;
   uint32_t limb_base;
   uint32_t load;              // NttLoad (explicit job lists only)
-  uint32_t pad_;
+  uint32_t store;             // NttStore (explicit job lists, forward transforms only)
   const BarrettConst* bc;     // per limb (MUL, DOT)
-  const RescaleConst* rc;     // per output limb at the input's level (RESCALE)
+  const RescaleConst* rc;     // per limb at the input's level (REDUCE, RESCALE stores)
   const uint64_t* key;        // secret key, L x N (DOT)
 };
 
