@@ -15,7 +15,9 @@ LoRA deltas per token; value = deltas/s.
 Also measured in the same run:
   * roofline: the batched NTT (64 polynomials x 4 limbs, N = 16384, forward
     and inverse as separate launches), timed with HIP events on the engine's
-    stream; algorithmic bytes = read + write of every limb-polynomial;
+    stream; algorithmic bytes = read + write of every limb-polynomial; the
+    same round trip at N = 32768 (reference chain for that degree) is
+    reported beside it as ntt_n32768;
   * parity: one layer of the timed pass re-run on the CPU oracle (bit-exact
     ciphertexts, deltas within 1e-3 relative), the NTT round trip and a
     forward transform checked against the oracle;
@@ -84,7 +86,7 @@ class DeviceInputs:
 
         self.ctx, self.L, self.lora = ctx, _lib.load(), lora
         self.steps = len(hidden_by_step)
-        self.h_stride = LAYERS * D * 8
+        self.h_stride = lora.n_inputs * lora.d * 8
         self.o_stride = lora.n_deltas * 8
         self.h, self.o = C.c_void_p(), C.c_void_p()
         _lib.check(self.L.th_dev_alloc(ctx._h, self.steps * self.h_stride, C.byref(self.h)))
@@ -112,14 +114,15 @@ class DeviceInputs:
 
 
 def ntt_roofline(ctx, reps=20):
-    """Batched NTT: 64 polys x 4 limbs at N=16384, forward and inverse launches."""
+    """Batched NTT: 64 polys x 4 limbs at the context's N, forward and inverse launches."""
     from provenloop_amd import _lib
     from oracle import oracle as orc
 
     L = _lib.load()
-    q = ctx.moduli
+    q = ctx.moduli[:4]
+    n = ctx.poly_mod_degree
     rng = np.random.default_rng(2)
-    host = np.stack([rng.integers(0, qq, (64, N), dtype=np.uint64) for qq in q], axis=1)  # [64, 4, N]
+    host = np.stack([rng.integers(0, qq, (64, n), dtype=np.uint64) for qq in q], axis=1)  # [64, 4, n]
     nbytes = host.nbytes
     dev = C.c_void_p()
     _lib.check(L.th_dev_alloc(ctx._h, nbytes, C.byref(dev)))
@@ -146,7 +149,7 @@ def ntt_roofline(ctx, reps=20):
     f, i = float(np.median(fwd_ms)), float(np.median(inv_ms))
     per_launch = 2 * nbytes  # read + write of every limb-polynomial
     return {
-        "polys": 64, "limbs": 4, "N": N, "bytes_per_launch": per_launch,
+        "polys": 64, "limbs": 4, "N": n, "bytes_per_launch": per_launch,
         "fwd_ms": f, "inv_ms": i,
         "fwd_GBs": per_launch / (f * 1e-3) / 1e9, "inv_GBs": per_launch / (i * 1e-3) / 1e9,
         "roundtrip_ms": f + i, "roundtrip_GBs": 2 * per_launch / ((f + i) * 1e-3) / 1e9,
@@ -276,18 +279,173 @@ NTT_CHAINS = {
 }
 
 
-def ntt_only(chain="default"):
+def ntt_only(chain="default", n=N):
     from provenloop_amd import tensafe_he
 
     q = NTT_CHAINS[chain]
-    ctx = tensafe_he.CkksContext(N) if q is None else tensafe_he.CkksContext(N, moduli=q)
+    if q is not None and n != N:
+        raise SystemExit("--ntt-chain other than default is defined for N=16384 only")
+    ctx = tensafe_he.CkksContext(n) if q is None else tensafe_he.CkksContext(n, moduli=q)
     ntt = ntt_roofline(ctx, reps=5)
     copy_ms = copy_calibration(ctx, ntt["bytes_per_launch"] // 2)
     print(json.dumps({
-        "metric": "batched NTT achieved GB/s (64 polys x 4 limbs, N=16384)",
+        "metric": f"batched NTT achieved GB/s (64 polys x 4 limbs, N={n})",
         "chain": chain, "moduli": ctx.moduli,
         "ntt": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in ntt.items()},
         "copy_calibration": {"bytes": ntt["bytes_per_launch"] // 2, "ms": round(copy_ms, 4)},
+    }), flush=True)
+
+
+# ------------------------------------------------------------------ secondary workloads
+def _timed_sessions(ctx, lora, sessions, dev_by_session, steps, warmup, seeds_fn):
+    """Time `steps` steps; a step queues one token of every session (its own keys,
+    HBM-resident inputs and outputs) and synchronises the stream once."""
+    for w in range(warmup):
+        for s, (pk, sk) in enumerate(sessions):
+            dev_by_session[s].run(pk, sk, steps + w, seeds_fn(s, 10_000 + w))
+    ctx.sync()
+    seeds = {(s, t): seeds_fn(s, t) for s in range(len(sessions)) for t in range(steps)}
+    t0 = time.perf_counter()
+    for t in range(steps):
+        for s, (pk, sk) in enumerate(sessions):
+            dev_by_session[s].run(pk, sk, t, seeds[(s, t)])
+        ctx.sync()
+    return time.perf_counter() - t0
+
+
+def run_moe(args):
+    """CryptoMOE variant of the per-token pass: 3 rank-16 expert adapters per
+    projection, softmax gate over a seeded logit vector per projection, the
+    experts' products combined with ct_add, then rescale and one batched
+    decrypt (th_lora_create_moe)."""
+    from oracle import oracle as orc
+    from provenloop_amd import tensafe_he, zero_moai
+
+    K = 3
+    rng = np.random.default_rng(4321)
+    proj, gates = [], []
+    for l in range(LAYERS):
+        for j, o in enumerate((D, D_V)):
+            proj.append((l, rng.normal(size=(K, RANK, D)) * 0.02, rng.normal(size=(K, o, RANK)) * 0.02))
+            gates.append(zero_moai.softmax_gate(1000 * l + j, K))
+    gates = np.array(gates)
+    ctx = tensafe_he.CkksContext(N)
+    sk = ctx.keygen(seed=11)
+    pk = ctx.keygen_public(sk, seed=22)
+    lora = zero_moai.LoraSet(ctx, LAYERS, proj, gates=gates)
+    order = list(range(args.steps)) + [10_000 + w for w in range(args.warmup)]
+    hidden = {t: hidden_states(t) for t in order}
+    dev = DeviceInputs(ctx, lora, [hidden[t] for t in order])
+    elapsed = _timed_sessions(ctx, lora, [(pk, sk)], [dev], args.steps, args.warmup, lambda s, t: seeds_for(t))
+    # parity: layer 0 of the last token against the oracle's literal k products + ct_add
+    last = args.steps - 1
+    flat = dev.deltas(last)
+    ref = orc.Context(N)
+    rsk = ref.keygen(11)
+    rpk = ref.keygen_public(rsk, 22)
+    S, cols = N // 2, (N // 2) // D
+    rct = ref.encrypt_pk(zero_moai.replicate(hidden[last][0], S, D), rpk, seeds_for(last)[0])
+    rel = []
+    for j in range(2):
+        _, A, Bm = proj[j]
+        g = gates[j]
+        packs = [zero_moai.pack_rows(A[x], S) for x in range(K)]
+        inter = np.zeros(RANK)
+        for b in range(len(packs[0])):
+            acc = None
+            for x in range(K):
+                prod = ref.ct_pt_mul(rct, g[x] * packs[x][b])
+                acc = prod if acc is None else ref.ct_add(acc, prod)
+            dec = ref.decrypt(ref.rescale(acc), rsk)
+            n = min(cols, RANK - b * cols)
+            inter[b * cols:b * cols + n] = [np.sum(dec[c * D:(c + 1) * D]) for c in range(n)]
+        e = sum(g[x] * Bm[x] for x in range(K)) @ inter
+        gj = flat[lora.offsets[j]:lora.offsets[j + 1]]
+        rel.append(float(np.linalg.norm(gj - e) / np.linalg.norm(e)))
+    dev.free()
+    deltas = LAYERS * 2 * args.steps
+    print(json.dumps({
+        "metric": "encrypted LoRA deltas/s, CryptoMOE variant (3 experts per projection) at N=16384",
+        "value": round(deltas / elapsed, 3), "unit": "deltas/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True,
+        "dtype": "u64", "data": "synthetic (seeded N(0,1)*0.1 hidden states, N(0,0.02) expert A/B)",
+        "config": {"workload": "CryptoMOE per-token pass, Qwen2.5-1.5B shape: 28 layers x {q,v} x 3 rank-16 "
+                               "experts, softmax gate per projection from a seeded logit vector, gate folded into "
+                               "each expert's plaintext, expert products combined with ct_add, rescale, one "
+                               "batched decrypt per token; hidden states and deltas resident in HBM",
+                   "experts": K, "N": N},
+        "parity": {"delta_rel_err_max_layer0": max(rel)},
+    }), flush=True)
+
+
+def run_saturation(args):
+    """Saturation run at Qwen2.5-7B shape: 32 sessions (own keys), hidden 3584, 28
+    layers x {q,k,v,o}, rank 32, N=32768 on the 8-limb chain; one step = one
+    token of every session, queued back to back with one synchronisation."""
+    from oracle import oracle as orc
+    from provenloop_amd import tensafe_he, zero_moai
+    from provenloop_amd.params import CHAIN_N32768_L8
+
+    n, d, rank, sessions, layers = 32768, 3584, 32, 32, 28
+    d_out = {"q": 3584, "k": 512, "v": 512, "o": 3584}
+    rng = np.random.default_rng(777)
+    proj = [(2 * l + (p == "o"), rng.normal(size=(rank, d)) * 0.02, rng.normal(size=(d_out[p], rank)) * 0.02)
+            for l in range(layers) for p in "qkvo"]
+    ctx = tensafe_he.CkksContext(n, moduli=CHAIN_N32768_L8)
+    lora = zero_moai.LoraSet(ctx, 2 * layers, proj)
+    keys = []
+    for s in range(sessions):
+        sk = ctx.keygen(seed=1000 + s)
+        keys.append((ctx.keygen_public(sk, seed=2000 + s), sk))
+    steps_all = args.steps + args.warmup
+
+    def hidden(s, t):
+        r = np.random.default_rng(100_003 * s + t)
+        return [(r.normal(size=d) * 0.1).astype(np.float32).astype(np.float64) for _ in range(2 * layers)]
+
+    devs = [DeviceInputs(ctx, lora, [hidden(s, t) for t in range(steps_all)]) for s in range(sessions)]
+
+    def seeds_fn(s, t):
+        return [(7_000_003 * s + 1_000_003 * t + i + 1) % (1 << 63) for i in range(2 * layers)]
+
+    elapsed = _timed_sessions(ctx, lora, keys, devs, args.steps, args.warmup, seeds_fn)
+    # parity: sessions 0 and 31, layer 27's q and o projections, last token, against the oracle
+    ref = orc.Context(n, CHAIN_N32768_L8)
+    S, cols = n // 2, (n // 2) // d
+    last = args.steps - 1
+    rel = []
+    for s in (0, sessions - 1):
+        flat = devs[s].deltas(last)
+        rsk = ref.keygen(1000 + s)
+        rpk = ref.keygen_public(rsk, 2000 + s)
+        hs, sd = hidden(s, last), seeds_fn(s, last)
+        for j in (4 * 27, 4 * 27 + 3):
+            i, A, Bm = proj[j]
+            rct = ref.encrypt_pk(zero_moai.replicate(hs[i], S, d), rpk, sd[i])
+            inter = np.zeros(rank)
+            for b, p in enumerate(zero_moai.pack_rows(A, S)):
+                dec = ref.decrypt(ref.rescale(ref.ct_pt_mul(rct, p)), rsk)
+                k = min(cols, rank - b * cols)
+                inter[b * cols:b * cols + k] = [np.sum(dec[c * d:(c + 1) * d]) for c in range(k)]
+            e = Bm @ inter
+            gj = flat[lora.offsets[j]:lora.offsets[j + 1]]
+            rel.append(float(np.linalg.norm(gj - e) / np.linalg.norm(e)))
+    for dv in devs:
+        dv.free()
+    per_step = sessions * 4 * layers
+    print(json.dumps({
+        "metric": "encrypted LoRA deltas/s, saturation at Qwen2.5-7B shape (32 sessions), N=32768, 8 limbs",
+        "value": round(per_step * args.steps / elapsed, 3), "unit": "deltas/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "dtype": "u64",
+        "data": "synthetic (seeded N(0,1)*0.1 hidden states, N(0,0.02) LoRA A/B, per-session seeded keys)",
+        "config": {"workload": "32 concurrent sessions, Qwen2.5-7B shape: 28 layers x {q,k,v,o}, hidden 3584, "
+                               "rank 32 (8 batches of 4 rows), N=32768, 8-limb chain, scale 2^40; per session "
+                               "token 56 encrypt_pk, 896 ct x pt + rescale, one batched decrypt; all sessions "
+                               "queued as one batch per step with one host synchronisation",
+                   "sessions": sessions, "N": n, "moduli": CHAIN_N32768_L8,
+                   "session_tokens_per_s": round(sessions * args.steps / elapsed, 3)},
+        "parity": {"delta_rel_err_max": max(rel)},
     }), flush=True)
 
 
@@ -304,13 +462,24 @@ def main():
     ap.add_argument("--ntt-chain", choices=sorted(NTT_CHAINS), default="default",
                     help="modulus chain of the --ntt-only launches: the default 4-limb chain, or four "
                          "60-bit (integer butterfly path) or four 40-bit (FP64 butterfly path) primes")
+    ap.add_argument("--ntt-n", type=int, choices=(16384, 32768), default=N,
+                    help="ring degree of the --ntt-only launches (reference chain for that degree)")
+    ap.add_argument("--workload", choices=("token", "moe", "saturation"), default="token",
+                    help="token: the per-token Qwen2.5-1.5B pass (the reported line); moe: its CryptoMOE "
+                         "variant; saturation: 32 sessions at Qwen2.5-7B shape on N=32768 with 8 limbs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by session/token "
               "with no cross-GPU exchange, so N GPUs scale the one-GPU figure)", file=sys.stderr)
         sys.exit(2)
     if args.ntt_only:
-        ntt_only(args.ntt_chain)
+        ntt_only(args.ntt_chain, args.ntt_n)
+        return
+    if args.workload == "moe":
+        run_moe(args)
+        return
+    if args.workload == "saturation":
+        run_saturation(args)
         return
 
     A, B = make_workload()
@@ -372,6 +541,11 @@ def main():
     rs_exact = all(np.array_equal(x, y) for x, y in zip(ctx.ct_download(g_r), cpu.ctx.ct_data(r_r)))
 
     ntt = ntt_roofline(ctx)
+    from provenloop_amd import tensafe_he
+
+    ctx32 = tensafe_he.CkksContext(2 * N)
+    ntt32 = ntt_roofline(ctx32)
+    del ctx32
 
     if args.no_cpu:
         cpu_single = cpu_multi = None
@@ -420,6 +594,8 @@ def main():
             "io": "hidden states from host memory, deltas to host memory (one device-to-host copy per token)",
         },
         "ntt": {k: (round(v, 5) if isinstance(v, float) else v) for k, v in ntt.items()},
+        "ntt_n32768": dict({k: (round(v, 5) if isinstance(v, float) else v) for k, v in ntt32.items()},
+                           frac=round(ntt32["roundtrip_GBs"] / HBM_PEAK_GBS, 4)),
         "parity": {
             "delta_rel_err_max": max(rel),
             "device_io_equals_host_io": dev_host_equal,
@@ -427,6 +603,8 @@ def main():
             "ctpt_rescale_bitexact": bool(rs_exact),
             "ntt_roundtrip_bitexact": ntt["roundtrip_bitexact"],
             "ntt_forward_bitexact": ntt["forward_matches_oracle"],
+            "ntt_n32768_roundtrip_bitexact": ntt32["roundtrip_bitexact"],
+            "ntt_n32768_forward_bitexact": ntt32["forward_matches_oracle"],
         },
         "cpu_baseline": None if cpu_multi is None else {
             "value": round(cpu_multi, 3),

@@ -194,6 +194,21 @@ typedef struct th_lora th_lora;
 int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
                    const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
                    th_lora** out);
+/* CryptoMOE set: n_experts adapters per projection, combined with gate
+ * weights. No counterpart in the reference, which routes each query to one
+ * adapter by keyword step-gates (inference_engine.py:1155-1171); the
+ * combination rule is this library's. Expert x of projection j has LoRA-A
+ * a[j*n_experts + x] (ranks[j] x d), LoRA-B b[j*n_experts + x]
+ * (d_out[j] x ranks[j]) and weight gates[j*n_experts + x]. Each expert's
+ * gate-scaled A rows g*A are packed and encoded as a plaintext of its own;
+ * the batch's ciphertext is the ct_add (ciphertext.rs:435-450) of the
+ * experts' ct x pt products (:422-429), bit for bit, so the decrypted
+ * intermediate is sum_x g_x A_x h. The B side applies sum_x g_x B_x to it.
+ * gates == NULL (allowed only with n_experts == 1) is th_lora_create.
+ * Gate weights must be finite; n_experts is at most 64. */
+int th_lora_create_moe(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
+                       const uint32_t* ranks, const uint32_t* d_out, uint32_t n_experts, const double* gates,
+                       const double* const* a, const double* const* b, th_lora** out);
 int th_lora_free(th_lora* set);
 /* n_deltas = sum of d_out (length of th_lora_deltas' output), n_batches =
  * number of plaintext batches, cols = segments per batch. Any may be NULL. */

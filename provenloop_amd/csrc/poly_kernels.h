@@ -65,6 +65,9 @@ hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_li
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
                             uint32_t n, hipStream_t s);
+// dst (nb x L x N) = per-batch sums mod q of k consecutive plaintexts in src (nb*k x L x N).
+hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, uint32_t k, uint32_t nb, uint32_t L,
+                         uint32_t n, hipStream_t s);
 // pk (optional): the public key [b | a] for every job instead of the jobs' fields.
 hipError_t launch_encrypt_combine(const EncCombineJob* jobs, uint32_t njobs, const BarrettConst* bc,
                                   uint32_t n, uint32_t L, hipStream_t s, const uint64_t* pk = nullptr);

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <new>
@@ -1360,8 +1361,15 @@ void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, Nt
   HIPCHK(launch_ntt((int)c->logn, inverse, a, n, c->stream));
 }
 
+// k experts per projection. Expert x of projection j has A = a[j * k + x],
+// B = b[j * k + x] and gate weight gates[j * k + x]; gates == nullptr (k == 1)
+// is a plain LoRA set.
+// Each packed batch holds, per expert, the gate-scaled A rows; the k encoded
+// plaintexts of a batch are folded into one (launch_pt_sum), which makes the
+// batch's product the ct_add of the k experts' products, bit for bit. The
+// B side applies sum_x g_x B_x to the decrypted intermediate.
 void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, const uint32_t* d_out,
-                const double* const* a, const double* const* b) {
+                uint32_t k, const double* gates, const double* const* a, const double* const* b) {
   th_ctx* c = set->ctx;
   const uint32_t N = c->N, S = N / 2, L = c->L, d = set->d, cols = set->cols;
   const size_t P = poly_bytes(c);
@@ -1375,13 +1383,34 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     const uint32_t nb = (ranks[j] + cols - 1) / cols;
     bj[j] = LoraBJob{nullptr, d_out[j], ranks[j], (uint32_t)batch_input.size(), 0, out_off};
     for (uint32_t bt = 0; bt < nb; ++bt) {
-      packed.resize(packed.size() + S, 0.0);
-      double* p = packed.data() + packed.size() - S;
-      for (uint32_t i = 0; i < cols && bt * cols + i < ranks[j]; ++i)
-        memcpy(p + (size_t)i * d, a[j] + (size_t)(bt * cols + i) * d, (size_t)d * 8);
+      for (uint32_t x = 0; x < k; ++x) {
+        const double* ax = a[(size_t)j * k + x];
+        packed.resize(packed.size() + S, 0.0);
+        double* p = packed.data() + packed.size() - S;
+        for (uint32_t i = 0; i < cols && bt * cols + i < ranks[j]; ++i) {
+          const double* row = ax + (size_t)(bt * cols + i) * d;
+          if (!gates) {
+            memcpy(p + (size_t)i * d, row, (size_t)d * 8);
+          } else {
+            const double g = gates[(size_t)j * k + x];
+            for (uint32_t t = 0; t < d; ++t) p[(size_t)i * d + t] = g * row[t];
+          }
+        }
+      }
       batch_input.push_back(input_of[j]);
     }
-    bmat.insert(bmat.end(), b[j], b[j] + (size_t)d_out[j] * ranks[j]);
+    const size_t bn = (size_t)d_out[j] * ranks[j];
+    if (!gates) {
+      bmat.insert(bmat.end(), b[j], b[j] + bn);
+    } else {
+      std::vector<double> mix(bn, 0.0);
+      for (uint32_t x = 0; x < k; ++x) {
+        const double g = gates[(size_t)j * k + x];
+        const double* bx = b[(size_t)j * k + x];
+        for (size_t t = 0; t < bn; ++t) mix[t] += g * bx[t];
+      }
+      bmat.insert(bmat.end(), mix.begin(), mix.end());
+    }
     out_off += d_out[j];
     set->max_d_out = std::max(set->max_d_out, d_out[j]);
   }
@@ -1421,12 +1450,15 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->d_sample = persist(set, sj);
     set->d_comb = persist(set, cj);
   }
-  // encode the plaintext batches (th_encode_to_ntt of each packed vector)
+  // encode the plaintext batches (th_encode_to_ntt of each packed vector); with
+  // experts, fold each batch's k plaintexts into one
   {
     OpScope sc(c);
     const double* z = sc.up(packed);
-    queue_encode(sc, z, nb, nullptr, nullptr, nullptr, set->pts, (size_t)L * N);
-    ntt_strided(c, false, set->pts, set->pts, nb * L, L);
+    uint64_t* dst = k == 1 ? set->pts : (uint64_t*)sc.dev((size_t)nb * k * L * P);
+    queue_encode(sc, z, nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
+    ntt_strided(c, false, dst, dst, nb * k * L, L);
+    if (k > 1) HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
     HIPCHK(hipStreamSynchronize(c->stream));  // the scope's buffers return to the pool
   }
   // per-token job lists
@@ -1502,19 +1534,24 @@ void free_lora(th_lora* set) {
 
 extern "C" {
 
-int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
-                   const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
-                   th_lora** out) {
+int th_lora_create_moe(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
+                       const uint32_t* ranks, const uint32_t* d_out, uint32_t n_experts, const double* gates,
+                       const double* const* a, const double* const* b, th_lora** out) {
   return guarded([&] {
     TH_LOCK(ctx);
     need(out != nullptr, "null output");
     need(n_inputs >= 1 && n_proj >= 1, "need at least one input and one projection");
+    need(n_experts >= 1 && n_experts <= 64, "n_experts must be in [1, 64]");
+    need(n_experts == 1 || gates != nullptr, "null gates");  // th_lora_create passes none
     need(d >= 1 && d <= ctx->N / 2, "d must be in [1, N/2]");
     need(input_of && ranks && d_out && a && b, "null argument");
     for (uint32_t j = 0; j < n_proj; ++j) {
       need(input_of[j] < n_inputs, "input_of index out of range");
       need(ranks[j] >= 1 && d_out[j] >= 1, "ranks and d_out must be positive");
-      need(a[j] && b[j], "null LoRA matrix");
+      for (uint32_t x = 0; x < n_experts; ++x) {
+        need(a[(size_t)j * n_experts + x] && b[(size_t)j * n_experts + x], "null LoRA matrix");
+        if (gates) need(std::isfinite(gates[(size_t)j * n_experts + x]), "gate weights must be finite");
+      }
     }
     th_lora* set = new th_lora{};
     set->ctx = ctx;
@@ -1523,7 +1560,7 @@ int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, 
     set->n_proj = n_proj;
     set->cols = (ctx->N / 2) / d;  // inference_engine.py:1258
     try {
-      build_lora(set, input_of, ranks, d_out, a, b);
+      build_lora(set, input_of, ranks, d_out, n_experts, gates, a, b);
     } catch (...) {
       (void)hipStreamSynchronize(ctx->stream);
       free_lora(set);
@@ -1531,6 +1568,12 @@ int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, 
     }
     *out = set;
   });
+}
+
+int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
+                   const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
+                   th_lora** out) {
+  return th_lora_create_moe(ctx, n_inputs, d, n_proj, input_of, ranks, d_out, 1, nullptr, a, b, out);
 }
 
 int th_lora_free(th_lora* set) {

@@ -122,6 +122,18 @@ def lora_deltas(ctx: CkksContext, pk: TenSafePublicKey, sk: TenSafeSecretKey, hi
     return deltas, inter
 
 
+def softmax_gate(seed: int, n_experts: int) -> np.ndarray:
+    """CryptoMOE gate: softmax over a seeded logit vector.
+
+    The reference routes each query to one adapter by keyword step-gates
+    (inference_engine.py:1155-1171) and has no gated combination; this rule
+    is the library's own: logits ~ N(0, 1) from numpy's PCG64 stream seeded
+    with `seed`, g = exp(l - max l) / sum exp(l - max l)."""
+    logits = np.random.default_rng(seed).standard_normal(n_experts)
+    w = np.exp(logits - logits.max())
+    return w / w.sum()
+
+
 class LoraSet:
     """LoRA projections resident on the device (th_lora_create).
 
@@ -131,9 +143,16 @@ class LoraSet:
     the encrypted path for all of them with one stream synchronisation:
     encrypt_pk per input, ct x pt per packed batch, rescale, batched decrypt
     with segment sums and B @ intermediate, all on the GPU.
+
+    CryptoMOE (th_lora_create_moe): with `gates` [n_proj, k], lora_a is
+    [k, rank, d] and lora_b [k, d_out, rank] (k expert adapters per
+    projection). Each batch's ciphertext is then the ct_add of the k
+    experts' products with their gate-scaled plaintexts g_x A_x, so the
+    decrypted intermediate is sum_x g_x A_x h, and the deltas are
+    (sum_x g_x B_x) @ intermediate.
     """
 
-    def __init__(self, ctx: CkksContext, n_inputs: int, projections):
+    def __init__(self, ctx: CkksContext, n_inputs: int, projections, gates=None):
         self._ctx = ctx
         self._lib = _lib.load()
         projections = list(projections)
@@ -142,23 +161,41 @@ class LoraSet:
         self.n_inputs = int(n_inputs)
         A = [np.ascontiguousarray(a, np.float64) for _, a, _ in projections]
         B = [np.ascontiguousarray(b, np.float64) for _, _, b in projections]
-        d = A[0].shape[1]
+        if gates is None:
+            k = 1
+            A = [a[None] for a in A]
+            B = [b[None] for b in B]
+        else:
+            G = np.ascontiguousarray(gates, np.float64)
+            if G.ndim != 2 or G.shape[0] != len(A):
+                raise ValueError("gates must be [n_proj, n_experts]")
+            k = G.shape[1]
+        if any(a.ndim != 3 or a.shape[0] != k for a in A) or any(b.ndim != 3 or b.shape[0] != k for b in B):
+            raise ValueError("with gates, lora_a must be [k, rank, d] and lora_b [k, d_out, rank]")
+        d = A[0].shape[2]
         for a, b in zip(A, B):
-            if a.ndim != 2 or a.shape[1] != d:
+            if a.shape[2] != d:
                 raise ValueError("every lora_a must be [rank, d] with the same d")
-            if b.ndim != 2 or b.shape[1] != a.shape[0]:
+            if b.shape[2] != a.shape[1]:
                 raise ValueError("lora_b must be [d_out, rank]")
         self.d = d
-        self.d_out = [b.shape[0] for b in B]
+        self.n_experts = k
+        self.d_out = [b.shape[1] for b in B]
         self.offsets = np.concatenate([[0], np.cumsum(self.d_out)]).astype(int)
         inp = np.array([int(i) for i, _, _ in projections], np.uint32)
-        ranks = np.array([a.shape[0] for a in A], np.uint32)
+        ranks = np.array([a.shape[1] for a in A], np.uint32)
         dout = np.array(self.d_out, np.uint32)
-        aptr = (C.c_void_p * len(A))(*[a.ctypes.data for a in A])
-        bptr = (C.c_void_p * len(B))(*[b.ctypes.data for b in B])
+        aptr = (C.c_void_p * (len(A) * k))(*[a[x].ctypes.data for a in A for x in range(k)])
+        bptr = (C.c_void_p * (len(B) * k))(*[b[x].ctypes.data for b in B for x in range(k)])
+        self._keep = (A, B)
         out = C.c_void_p()
-        _lib.check(self._lib.th_lora_create(ctx._h, self.n_inputs, d, len(A), _lib.ptr(inp), _lib.ptr(ranks),
-                                            _lib.ptr(dout), aptr, bptr, C.byref(out)))
+        if gates is None:
+            _lib.check(self._lib.th_lora_create(ctx._h, self.n_inputs, d, len(A), _lib.ptr(inp), _lib.ptr(ranks),
+                                                _lib.ptr(dout), aptr, bptr, C.byref(out)))
+        else:
+            _lib.check(self._lib.th_lora_create_moe(ctx._h, self.n_inputs, d, len(A), _lib.ptr(inp),
+                                                    _lib.ptr(ranks), _lib.ptr(dout), k, _lib.ptr(G), aptr, bptr,
+                                                    C.byref(out)))
         self._h = out
         nd, nb, cols = C.c_uint64(), C.c_uint32(), C.c_uint32()
         _lib.check(self._lib.th_lora_info(self._h, C.byref(nd), C.byref(nb), C.byref(cols)))

@@ -96,15 +96,18 @@ def test_ntt_large_batch_matches_oracle(n, polys):
     assert np.array_equal(ctx.ntt_inverse(fwd), x)
 
 
-def test_ntt_batched_microbench_shape(eng16):
-    """64 polynomials x 4 limbs at N=16384 (the batched round-trip workload)."""
+@pytest.mark.parametrize("n", [16384, 32768])
+def test_ntt_batched_microbench_shape(n):
+    """64 polynomials x 4 limbs (the batched round-trip workload) on the reference chain for N."""
+    q = orc.default_chain(n)
+    ctx = tensafe_he.CkksContext(n)
     rng = np.random.default_rng(7)
-    x = np.stack([rng.integers(0, q, (64, 16384), dtype=np.uint64) for q in Q16384], axis=1)
-    fwd = eng16.ntt_forward(x)
+    x = np.stack([rng.integers(0, qq, (64, n), dtype=np.uint64) for qq in q], axis=1)
+    fwd = ctx.ntt_forward(x)
     for p in (0, 31, 63):
-        for l, q in enumerate(Q16384):
-            assert np.array_equal(fwd[p, l], orc.ntt_forward(x[p, l], q))
-    assert np.array_equal(eng16.ntt_inverse(fwd), x)
+        for l, qq in enumerate(q):
+            assert np.array_equal(fwd[p, l], orc.ntt_forward(x[p, l], qq))
+    assert np.array_equal(ctx.ntt_inverse(fwd), x)
 
 
 # ------------------------------------------------------------------ keys and encryption
