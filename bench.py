@@ -128,15 +128,18 @@ def ntt_roofline(ctx, reps=20):
     _lib.check(L.th_dev_alloc(ctx._h, nbytes, C.byref(dev)))
     _lib.check(L.th_memcpy_h2d(ctx._h, dev, _lib.ptr(host), nbytes))
     t_f, t_i = C.c_float(), C.c_float()
-    # warm-up round trips, then timed launches (each round trip leaves the data unchanged)
+    # warm-up round trips, then timed runs of `inner` back-to-back forward launches
+    # followed by as many inverse launches (which bring the data back exactly);
+    # each sample is the average launch time of one run
+    inner = 10
     for _ in range(3):
         _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 0, 1, C.byref(t_f)))
         _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 1, 1, C.byref(t_i)))
     fwd_ms, inv_ms = [], []
     for _ in range(reps):
-        _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 0, 1, C.byref(t_f)))
+        _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 0, inner, C.byref(t_f)))
         fwd_ms.append(t_f.value)
-        _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 1, 1, C.byref(t_i)))
+        _lib.check(L.th_ntt_time(ctx._h, dev, 64, 4, 1, inner, C.byref(t_i)))
         inv_ms.append(t_i.value)
     back = np.empty_like(host)
     _lib.check(L.th_memcpy_d2h(ctx._h, _lib.ptr(back), dev, nbytes))

@@ -15,14 +15,27 @@
 // split kernels move the data twice but keep many wavefronts per CU. The
 // whole-polynomial kernel's time grows in steps of one round of workgroups
 // (one per CU); measured on MI355X at N = 16384 it wins for one round (256
-// transforms: 41 us vs 49 us) and the split kernels win from 384 transforms
-// on (1792: 200 us vs 256 us). So batches of at most NTT_WHOLE_MAX_JOBS = 256
-// (the CU count) use the first, larger ones the second. T = N/16 threads hold 16 coefficients each
-// in registers; a register pass performs 4 butterfly stages on the
+// transforms: 40 us vs 46 us forward) and the split kernels win from 384
+// transforms on (1792: 197 us vs 256 us). So batches of at most
+// NTT_WHOLE_MAX_JOBS = 256 (the CU count) use the first, larger ones the
+// second.
+//
+// Whole-polynomial kernel: T = N/16 threads hold 16 coefficients each in
+// registers; a register pass performs up to 4 butterfly stages on the
 // register-resident bits, and between passes the coefficients are exchanged
 // through LDS (one padding slot per 16 u64 spreads the strided patterns over
-// the banks). Global loads and stores are lane-contiguous (lane t touches
-// element t + k*T).
+// the banks). Only one exchange per transform spans the workgroup: in every
+// layout whose register window starts at or below bit 6, wavefront w holds
+// the 1024 elements whose bits >= 10 equal w, so the exchanges among those
+// layouts stay inside a wavefront (its own LDS slice, no barrier) and the
+// wavefronts drift apart, overlapping one another's twiddle loads, arithmetic
+// and stores. Forward: bits 13..10 in the lane-contiguous load layout, the
+// workgroup exchange, then bits 9..0 in wavefront-local passes, stored from
+// the wavefront-contiguous layout. Inverse: the mirror image, with the first
+// stage's twiddles loaded before the coefficients. Passes whose twiddle
+// indices are uniform across a wavefront read them with scalar loads. The
+// fused load/store operations are template parameters, so each kernel
+// carries only its own.
 #include "ntt_arith.h"
 
 namespace th {
@@ -42,10 +55,15 @@ struct Shape {
   static constexpr int T = N / E;
   static constexpr int LDS_ELEMS = N + (N >> 4);
   static constexpr int COAL_LO = LOGN - LE;  // register bits on top: lane-contiguous global access
+  static constexpr int WAVE_LO = 6;          // lane-contiguous inside each wavefront's 1024 elements
 };
 
 // Element index held by thread `tid` in register k, for the layout whose
-// register bits are [LO, LO + LE).
+// register bits are [LO, LO + LE). In every layout with LO <= 6, wavefront
+// w = tid >> 6 holds exactly the 1024 elements whose bits >= 10 equal w
+// (tid bits [LO, 6) land on element bits [LO + 4, 10), tid bits >= 6 on
+// bits >= 10), so an exchange between two such layouts stays inside the
+// wavefront and its LDS region, and needs no workgroup barrier.
 template <int LE, int LO>
 __device__ __forceinline__ uint32_t elem(uint32_t tid, uint32_t k) {
   return (tid & ((1u << LO) - 1)) | ((tid >> LO) << (LO + LE)) | (k << LO);
@@ -53,26 +71,42 @@ __device__ __forceinline__ uint32_t elem(uint32_t tid, uint32_t k) {
 
 __device__ __forceinline__ uint32_t phys(uint32_t j) { return j + (j >> 4); }
 
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Re-distribute the coefficients from layout LO_S to layout LO_D through LDS.
 template <int LOGN, int LO_S, int LO_D, class V>
 __device__ __forceinline__ void exchange(V (&x)[Shape<LOGN>::E], V* lds, uint32_t tid) {
   using S = Shape<LOGN>;
+  constexpr bool WAVE = LO_S <= S::WAVE_LO && LO_D <= S::WAVE_LO;
 #pragma unroll
   for (int k = 0; k < S::E; ++k) lds[phys(elem<S::LE, LO_S>(tid, k))] = x[k];
-  __syncthreads();
+  if constexpr (WAVE) wave_sync(); else __syncthreads();
 #pragma unroll
   for (int k = 0; k < S::E; ++k) x[k] = lds[phys(elem<S::LE, LO_D>(tid, k))];
-  __syncthreads();
+  if constexpr (WAVE) wave_sync(); else __syncthreads();
+}
+
+// Element bits above the register window of layout LO for this thread; the
+// same for a whole wavefront when LO >= 6 (then read through readfirstlane so
+// that the pass's twiddle loads are scalar).
+template <int LOGN, int LO>
+__device__ __forceinline__ uint32_t jhi_of(uint32_t tid) {
+  uint32_t h = tid >> LO;
+  if constexpr (LO >= Shape<LOGN>::WAVE_LO) h = __builtin_amdgcn_readfirstlane(h);
+  return h << (LO + Shape<LOGN>::LE);
 }
 
 // ------------------------------------------------------------------ register passes
 // Forward stages for bits BHI down to BLO on the layout with register bits [LO, LO+LE).
-template <int LOGN, int LO, int BHI, int BLO, bool FIRST, class A>
+template <int LOGN, int LO, int BHI, int BLO, class A>
 __device__ __forceinline__ void fwd_pass(typename A::V (&x)[Shape<LOGN>::E], uint32_t tid,
                                          const typename A::Tw* __restrict__ tw, const A& ar) {
   using S = Shape<LOGN>;
-  // thread's element bits above the register window (zero for the first pass)
-  const uint32_t jhi = FIRST ? 0u : ((tid >> LO) << (LO + S::LE));
+  const uint32_t jhi = jhi_of<LOGN, LO>(tid);
 #pragma unroll
   for (int b = BHI; b >= BLO; --b) {
     const int rb = b - LO;
@@ -87,12 +121,14 @@ __device__ __forceinline__ void fwd_pass(typename A::V (&x)[Shape<LOGN>::E], uin
   }
 }
 
+// Inverse stages for bits BLO up to BHI. `pre` (may be null) holds the twiddles
+// of stage BLO, loaded ahead of time.
 template <int LOGN, int LO, int BLO, int BHI, class A>
 __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uint32_t tid,
                                          const typename A::Tw* __restrict__ tw, const A& ar,
-                                         const LimbConst& lc) {
+                                         const LimbConst& lc, const typename A::Tw* pre) {
   using S = Shape<LOGN>;
-  const uint32_t jhi = (tid >> LO) << (LO + S::LE);
+  const uint32_t jhi = jhi_of<LOGN, LO>(tid);
 #pragma unroll
   for (int b = BLO; b <= BHI; ++b) {
     const int rb = b - LO;
@@ -104,7 +140,8 @@ __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uin
       if (b == LOGN - 1) {
         ar.inv_last(x[k], x[k2], lc);
       } else {
-        const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+        const uint32_t m = (uint32_t)(k >> (rb + 1));
+        const typename A::Tw t = (pre && b == BLO) ? pre[m] : tw[base | m];
         ar.inv(x[k], x[k2], t);
       }
     }
@@ -116,39 +153,63 @@ __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uin
 }
 
 // Remaining forward passes: bits [TOP-1 .. 0] still to do, registers in layout CUR_LO.
-template <int LOGN, int TOP, int CUR_LO, bool FIRST, class A>
+// Windows step down from the top; once below bit 10 every exchange is inside a
+// wavefront, so after the first exchange the wavefronts run without barriers.
+template <int LOGN, int TOP, int CUR_LO, class A>
 __device__ __forceinline__ void fwd_passes(typename A::V (&x)[Shape<LOGN>::E], typename A::V* lds,
                                            uint32_t tid, const typename A::Tw* tw, const A& ar) {
   using S = Shape<LOGN>;
   if constexpr (TOP > 0) {
     constexpr int LO = TOP - S::LE > 0 ? TOP - S::LE : 0;
     if constexpr (LO != CUR_LO) exchange<LOGN, CUR_LO, LO>(x, lds, tid);
-    fwd_pass<LOGN, LO, TOP - 1, LO, FIRST, A>(x, tid, tw, ar);
-    fwd_passes<LOGN, LO, LO, false, A>(x, lds, tid, tw, ar);
+    fwd_pass<LOGN, LO, TOP - 1, LO, A>(x, tid, tw, ar);
+    fwd_passes<LOGN, LO, LO, A>(x, lds, tid, tw, ar);
   } else {
-    // restage to the lane-contiguous layout for the store
-    if constexpr (CUR_LO != S::COAL_LO) exchange<LOGN, CUR_LO, S::COAL_LO>(x, lds, tid);
+    // restage inside each wavefront to the wavefront-contiguous layout for the store
+    if constexpr (CUR_LO != S::WAVE_LO) exchange<LOGN, CUR_LO, S::WAVE_LO>(x, lds, tid);
   }
+}
+
+// Window of the inverse pass that starts at bit BOT: below bit 10 the window
+// starts at most at bit 6 (exchanges inside a wavefront), above it the
+// lane-contiguous layout is reached with the one workgroup-wide exchange.
+template <int LOGN>
+constexpr int inv_lo(int bot) {
+  return bot < 10 ? (bot < Shape<LOGN>::WAVE_LO ? bot : Shape<LOGN>::WAVE_LO)
+                  : (bot < Shape<LOGN>::COAL_LO ? bot : Shape<LOGN>::COAL_LO);
+}
+template <int LOGN>
+constexpr int inv_hi(int bot) {
+  return inv_lo<LOGN>(bot) + Shape<LOGN>::LE - 1 < LOGN - 1 ? inv_lo<LOGN>(bot) + Shape<LOGN>::LE - 1 : LOGN - 1;
+}
+// The layout the inverse passes end in.
+template <int LOGN>
+constexpr int inv_end_lo() {
+  int bot = 0, lo = 0;
+  while (bot < LOGN) {
+    lo = inv_lo<LOGN>(bot);
+    bot = inv_hi<LOGN>(bot) + 1;
+  }
+  return lo;
 }
 
 // Remaining inverse passes: bits [BOT .. LOGN-1] still to do.
 template <int LOGN, int BOT, int CUR_LO, class A>
 __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], typename A::V* lds,
                                            uint32_t tid, const typename A::Tw* tw, const A& ar,
-                                           const LimbConst& lc) {
-  using S = Shape<LOGN>;
+                                           const LimbConst& lc, const typename A::Tw* pre) {
   if constexpr (BOT < LOGN) {
-    constexpr int LO = BOT < S::COAL_LO ? BOT : S::COAL_LO;
-    constexpr int HI = LO + S::LE - 1;
+    constexpr int LO = inv_lo<LOGN>(BOT);
+    constexpr int HI = inv_hi<LOGN>(BOT);
     if constexpr (LO != CUR_LO) exchange<LOGN, CUR_LO, LO>(x, lds, tid);
-    inv_pass<LOGN, LO, BOT, HI, A>(x, tid, tw, ar, lc);
-    inv_passes<LOGN, HI + 1, LO, A>(x, lds, tid, tw, ar, lc);
+    inv_pass<LOGN, LO, BOT, HI, A>(x, tid, tw, ar, lc, pre);
+    inv_passes<LOGN, HI + 1, LO, A>(x, lds, tid, tw, ar, lc, nullptr);
   }
 }
 
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, class LOp, class SOp>
 __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                        const LimbConst& lc, const LoadOp& op, const StoreOp& so, void* lds_raw) {
+                                        const LimbConst& lc, const LOp& op, const SOp& so, void* lds_raw) {
   using S = Shape<LOGN>;
   const uint32_t tid = threadIdx.x;
   const A ar(lc);
@@ -156,30 +217,43 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, tid + k * S::T));
+    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, S::COAL_LO>(tid, k)));
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
-    fwd_passes<LOGN, LOGN, S::COAL_LO, true, A>(x, lds, tid, tw, ar);
+    fwd_passes<LOGN, LOGN, S::COAL_LO, A>(x, lds, tid, tw, ar);
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) dst[tid + k * S::T] = so(ar.fwd_store(x[k]), tid + k * S::T);
+    for (int k = 0; k < S::E; ++k) {
+      const uint32_t i = elem<S::LE, S::WAVE_LO>(tid, k);
+      dst[i] = so(ar.fwd_store(x[k]), i);
+    }
   } else {
-#pragma unroll
-    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, tid + k * S::T));
+    // the first pass (layout LO = 0, bits 0..3) needs the most distinct
+    // twiddles; its first stage's 8 are loaded before the coefficients so
+    // that their latency hides behind the coefficient loads
     const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
-    inv_passes<LOGN, 0, S::COAL_LO, A>(x, lds, tid, tw, ar, lc);
+    typename A::Tw pre[S::E / 2];
+    {
+      const uint32_t base = ((uint32_t)S::N | (tid << S::LE)) >> 1;
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) dst[tid + k * S::T] = ar.inv_store(x[k]);
+      for (int m = 0; m < S::E / 2; ++m) pre[m] = tw[base | (uint32_t)m];
+    }
+#pragma unroll
+    for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, S::WAVE_LO>(tid, k)));
+    inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, tw, ar, lc, pre);
+    constexpr int END = inv_end_lo<LOGN>();
+#pragma unroll
+    for (int k = 0; k < S::E; ++k) dst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
   }
 }
 
-template <int LOGN, bool INV>
+template <int LOGN, bool INV, uint32_t LD, uint32_t ST>
 __global__ __launch_bounds__(Shape<LOGN>::T) void ntt_kernel(NttArgs a) {
   extern __shared__ uint64_t lds[];
   const uint32_t job = blockIdx.x;
   const uint64_t* src;
   uint64_t* dst;
   uint32_t limb;
-  LoadOp op{};
-  StoreOp so{};
+  LoadOp<LD> op{};
+  StoreOp<ST> so{};
   if (a.jobs) {
     const NttJob jb = a.jobs[job];
     src = jb.src;
@@ -201,16 +275,19 @@ __global__ __launch_bounds__(Shape<LOGN>::T) void ntt_kernel(NttArgs a) {
 template <int LOGN, bool INV>
 static hipError_t launch_one(const NttArgs& a, uint32_t njobs, hipStream_t s) {
   using S = Shape<LOGN>;
-  static bool attr_set = false;
   const size_t lds = (size_t)S::LDS_ELEMS * 8;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)ntt_kernel<LOGN, INV>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((ntt_kernel<LOGN, INV>), dim3(njobs), dim3(S::T), lds, s, a);
-  return hipGetLastError();
+  return with_ops(INV, a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
+                  [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+                    static bool attr_set = false;  // one per instantiation
+                    if (!attr_set) {
+                      hipError_t e = hipFuncSetAttribute((const void*)ntt_kernel<LOGN, INV, LD, ST>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                      if (e != hipSuccess) return e;
+                      attr_set = true;
+                    }
+                    hipLaunchKernelGGL((ntt_kernel<LOGN, INV, LD, ST>), dim3(njobs), dim3(S::T), lds, s, a);
+                    return hipGetLastError();
+                  });
 }
 
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {

@@ -82,52 +82,77 @@ struct Fp64Arith {
   __device__ __forceinline__ V unraw(uint64_t x) const { return __builtin_bit_cast(double, x); }
 };
 
-// The operation fused into the coefficient load (NttLoad); `i` indexes the
+// The operation fused into the coefficient load (NttLoad), fixed at compile
+// time so that each kernel carries only its own operation; `i` indexes the
 // limb-polynomial, so src, aux and key are read at the same position.
+template <uint32_t LD>
 struct LoadOp {
-  uint32_t kind;
   const uint64_t* aux;
   const uint64_t* key;  // secret-key limb-poly (DOT)
   BarrettConst bc;
   RescaleConst rc;
   __device__ __forceinline__ uint64_t operator()(const uint64_t* __restrict__ src, uint32_t i) const {
     const uint64_t x = src[i];
-    switch (kind) {
-      case NTT_LOAD_MUL: return mulmod_barrett(x, aux[i], bc);
-      case NTT_LOAD_REDUCE: return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
-      case NTT_LOAD_DOT: return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
-      default: return x;
-    }
+    if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, aux[i], bc);
+    if constexpr (LD == NTT_LOAD_REDUCE) return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
+    if constexpr (LD == NTT_LOAD_DOT) return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
+    return x;
   }
 };
 
 // The operation fused into a forward transform's final store (NttStore).
+template <uint32_t ST>
 struct StoreOp {
-  uint32_t kind;
   const uint64_t* aux;
   const uint64_t* aux2;
   BarrettConst bc;
   RescaleConst rc;
   __device__ __forceinline__ uint64_t operator()(uint64_t y, uint32_t i) const {
-    if (kind == NTT_STORE_NONE) return y;
-    const uint64_t c = kind == NTT_STORE_MUL_RESCALE ? mulmod_barrett(aux[i], aux2[i], bc) : aux[i];
-    return csub(shoup_lazy(submod(c, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
+    if constexpr (ST == NTT_STORE_NONE) {
+      return y;
+    } else {
+      uint64_t c;
+      if constexpr (ST == NTT_STORE_MUL_RESCALE)
+        c = mulmod_barrett(aux[i], aux2[i], bc);
+      else
+        c = aux[i];
+      return csub(shoup_lazy(submod(c, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
+    }
   }
 };
 
 // Load and store operations of job `jb` in launch `a` for limb `limb`.
-__device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint32_t limb, uint32_t n, LoadOp& op,
-                                        StoreOp& so) {
-  op.kind = a.load;
+template <uint32_t LD, uint32_t ST>
+__device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint32_t limb, uint32_t n,
+                                        LoadOp<LD>& op, StoreOp<ST>& so) {
   op.aux = jb.aux;
-  if (a.load == NTT_LOAD_MUL || a.load == NTT_LOAD_DOT) op.bc = a.bc[limb];
-  if (a.load == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * n;
-  if (a.load == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
-  so.kind = a.store;
+  if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT) op.bc = a.bc[limb];
+  if constexpr (LD == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * n;
+  if constexpr (LD == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
   so.aux = jb.aux;
   so.aux2 = jb.aux2;
-  if (a.store != NTT_STORE_NONE) so.rc = a.rc[limb];
-  if (a.store == NTT_STORE_MUL_RESCALE) so.bc = a.bc[limb];
+  if constexpr (ST != NTT_STORE_NONE) so.rc = a.rc[limb];
+  if constexpr (ST == NTT_STORE_MUL_RESCALE) so.bc = a.bc[limb];
+}
+
+// Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
+// Only the pairs the engine issues are instantiated: forward (NONE, NONE),
+// (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT, NONE).
+template <class F>
+__host__ hipError_t with_ops(bool inverse, uint32_t load, uint32_t store, F&& f) {
+  if (!inverse) {
+    if (load == NTT_LOAD_NONE && store == NTT_STORE_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_REDUCE && store == NTT_STORE_RESCALE)
+      return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_RESCALE>();
+    if (load == NTT_LOAD_REDUCE && store == NTT_STORE_MUL_RESCALE)
+      return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_MUL_RESCALE>();
+    return hipErrorInvalidValue;
+  }
+  if (store != NTT_STORE_NONE) return hipErrorInvalidValue;
+  if (load == NTT_LOAD_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
+  if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();
+  if (load == NTT_LOAD_DOT) return f.template operator()<NTT_LOAD_DOT, NTT_STORE_NONE>();
+  return hipErrorInvalidValue;
 }
 
 }  // namespace th

@@ -113,9 +113,9 @@ __device__ __forceinline__ void wave_exchange(V (&x)[16], V* lds, From from, To 
 }
 
 // ------------------------------------------------------------------ column pass
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, class LOp>
 __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                            const LimbConst& lc, const LoadOp& op, uint32_t part, uint64_t* lds_raw) {
+                                            const LimbConst& lc, const LOp& op, uint32_t part, uint64_t* lds_raw) {
   using S = Split<LOGN>;
   constexpr int RB = S::RB, CB = S::CB, CW = S::CW, WL = 10 - RB;  // WL = log2(CW)
   const uint32_t l = threadIdx.x;
@@ -151,9 +151,9 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
 }
 
 // ------------------------------------------------------------------ row pass
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, class LOp, class SOp>
 __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                                         const LimbConst& lc, const LoadOp& op, const StoreOp& so, uint32_t part,
+                                         const LimbConst& lc, const LOp& op, const SOp& so, uint32_t part,
                                          uint64_t* lds_raw) {
   using S = Split<LOGN>;
   constexpr int CB = S::CB, M = (1 << (CB - 4)) - 1;
@@ -194,7 +194,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
 // the transform's input applies the fused load operation and the forward
 // row pass the fused store operation; otherwise passes read and write the
 // destination only.
-template <int LOGN, bool INV, bool COLUMN>
+template <int LOGN, bool INV, bool COLUMN, uint32_t LD, uint32_t ST>
 __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
   __shared__ uint64_t lds[S::LDS];
@@ -209,8 +209,8 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   const uint64_t* src;
   uint64_t* dst;
   uint32_t limb;
-  LoadOp op{};
-  StoreOp so{};
+  LoadOp<LD> op{};
+  StoreOp<ST> so{};
   if (a.jobs) {
     const NttJob jb = a.jobs[job];
     src = jb.src;
@@ -236,18 +236,25 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   }
 }
 
+// The pass that reads the transform's input (column pass forward, row pass
+// inverse) carries the load operation, the forward row pass the store
+// operation; the other pass is instantiated with none.
 template <int LOGN>
 static hipError_t launch_split_t(bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
   using S = Split<LOGN>;
   const dim3 grid(njobs * S::PARTS), block(64);
-  if (!inverse) {
-    hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true>), grid, block, 0, s, a);
-    hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false>), grid, block, 0, s, a);
-  } else {
-    hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false>), grid, block, 0, s, a);
-    hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, true>), grid, block, 0, s, a);
-  }
-  return hipGetLastError();
+  return with_ops(inverse, a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
+                  [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+                    if (!inverse) {
+                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, LD, NTT_STORE_NONE>), grid, block, 0, s, a);
+                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false, NTT_LOAD_NONE, ST>), grid, block, 0, s, a);
+                    } else {
+                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, LD, NTT_STORE_NONE>), grid, block, 0, s, a);
+                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, true, NTT_LOAD_NONE, NTT_STORE_NONE>), grid, block,
+                                         0, s, a);
+                    }
+                    return hipGetLastError();
+                  });
 }
 
 hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
