@@ -36,11 +36,11 @@ __device__ __forceinline__ double u128_to_f64(uint64_t hi, uint64_t lo) {
 // Decrypted coefficient j, centred (or CRT-combined and centred), as f64.
 __device__ __forceinline__ double coeff_centred(const DecodeJob& jb, const DecodeConst& dc, uint32_t j, uint32_t n) {
   if (!jb.crt) {
-    const uint64_t c = jb.m[j];
+    const uint64_t c = gld(jb.m)[j];
     return c > dc.half_q0 ? -((double)(dc.q0 - c)) : (double)c;
   }
   // ciphertext.rs:360-392
-  const uint64_t m0 = jb.m[j], m1 = jb.m[n + j];
+  const uint64_t m0 = gld(jb.m)[j], m1 = gld(jb.m)[n + j];
   const uint64_t m0q1 = m0 < dc.q1 ? m0 : mulmod_barrett(m0, 1, dc.b1);
   const uint64_t diff = m1 >= m0q1 ? m1 - m0q1 : dc.q1 - m0q1 + m1;
   const uint64_t k = csub(shoup_lazy(diff, dc.q0_inv_q1, dc.q0_inv_q1_s, dc.q1), dc.q1);
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_parts(const DecodeJob* _
   }
   __syncthreads();
   dit_stages_reg(re, im, lb, stage_re, stage_im);
-  double* out = jb.parts + (size_t)part * 2 * M;
+  const GMut<double> out = gst(jb.parts) + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[i];
     out[M + i] = im[i];
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* _
   const uint32_t S = n / 2;
   const uint32_t M = n >> LP;
   const DecodeJob jb = jobs[blockIdx.x];
-  const double* P = jb.parts;
+  const GPtr<double> P = gld(jb.parts);
   auto at = [&](uint32_t part, uint32_t i) { return Cx{P[(size_t)part * 2 * M + i], P[(size_t)part * 2 * M + M + i]}; };
   if constexpr (LP == 0) {
     for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) dec[k] = P[k];
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* _
   }
   __syncthreads();
   if (jb.out)
-    for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) jb.out[k] = dec[k];
+    for (uint32_t k = threadIdx.x; k < S; k += blockDim.x) gst(jb.out)[k] = dec[k];
   if (jb.seg) {
     // one wavefront per segment; lane-strided partial sums, then a fixed butterfly tree
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(DEC_THREADS) void k_decode_final(const DecodeJob* _
         if (base + i < S) acc += dec[base + i];
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-      if (lane == 0) jb.seg[sg] = acc;
+      if (lane == 0) gst(jb.seg)[sg] = acc;
     }
   }
 }
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void k_segsum_partial(const DecodeJob* __restr
   __syncthreads();
   if (threadIdx.x < cols) {
     const int c = threadIdx.x;
-    jb.parts[blockIdx.x * cols + c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
+    gst(jb.parts)[blockIdx.x * cols + c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
   }
 }
 
@@ -205,8 +205,8 @@ __global__ void k_segsum_final(const DecodeJob* __restrict__ jobs, uint32_t njob
   const DecodeJob jb = jobs[t / cols];
   const uint32_t c = t % cols;
   double s = 0.0;
-  for (uint32_t k = 0; k < SEGSUM_CHUNKS; ++k) s += jb.parts[k * cols + c];
-  jb.seg[c] = s / jb.scale;
+  for (uint32_t k = 0; k < SEGSUM_CHUNKS; ++k) s += gld(jb.parts)[k * cols + c];
+  gst(jb.seg)[c] = s / jb.scale;
 }
 
 hipError_t launch_segsum(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* W,

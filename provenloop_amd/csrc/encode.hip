@@ -26,7 +26,7 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   const uint32_t M = n >> LP;
   const uint32_t part = blockIdx.x;
   const EncodeJob jb = jobs[blockIdx.y];
-  const double* z = z_base ? z_base + (size_t)blockIdx.y * (jb.rep_d ? jb.rep_d : S) : jb.z;
+  const GPtr<double> z = gld(z_base ? z_base + (size_t)blockIdx.y * (jb.rep_d ? jb.rep_d : S) : jb.z);
   double* re = sh;
   double* im = sh + M;
   const uint32_t r = brv_bits(part, LP);
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   }
   __syncthreads();
   dit_stages_reg(re, im, lb, stage_re, stage_im);
-  double* out = jb.parts + (size_t)part * 2 * M;
+  const GMut<double> out = gst(jb.parts) + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[i];
     out[M + i] = im[i];
@@ -75,16 +75,16 @@ __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const Barr
   const double a_im = a.im * inv_n;
   const double coeff = a_re * twist_re[j] + a_im * twist_im[j];
   const int64_t m = round_sat_i64(coeff * 1099511627776.0);  // * 2^40 (params.rs:12)
-  const int64_t e0 = jb.e0 ? jb.e0[j] : 0;
+  const int64_t e0 = jb.e0 ? gld(jb.e0)[j] : 0;
+  const int64_t e1 = jb.e1 ? gld(jb.e1)[j] : 0;
+  const uint8_t u = jb.u ? gld(jb.u)[j] : 1;  // ciphertext.rs:261-266: 0 -> q-1, 1 -> 0, 2 -> 1
+  const GMut<uint64_t> dst = gst(jb.dst);
   for (uint32_t l = 0; l < L; ++l) {
     const BarrettConst c = bc[l];
     const uint64_t mm = signed_residue_dev(m, c);
-    jb.dst[(size_t)l * n + j] = jb.e0 ? csub(mm + signed_residue_dev(e0, c), c.q) : mm;
-    if (jb.e1) jb.dst[(size_t)(L + l) * n + j] = signed_residue_dev(jb.e1[j], c);
-    if (jb.u) {
-      const uint8_t u = jb.u[j];  // ciphertext.rs:261-266: 0 -> q-1, 1 -> 0, 2 -> 1
-      jb.dst[(size_t)(2 * L + l) * n + j] = u == 0 ? c.q - 1 : (u == 1 ? 0 : 1);
-    }
+    dst[(size_t)l * n + j] = jb.e0 ? csub(mm + signed_residue_dev(e0, c), c.q) : mm;
+    if (jb.e1) dst[(size_t)(L + l) * n + j] = signed_residue_dev(e1, c);
+    if (jb.u) dst[(size_t)(2 * L + l) * n + j] = u == 0 ? c.q - 1 : (u == 1 ? 0 : 1);
   }
 }
 
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
   const uint32_t n = 1u << logn;
   const uint32_t M = n >> LP;
   const EncodeJob jb = jobs[blockIdx.y];
-  const double* P = jb.parts;
+  const GPtr<double> P = gld(jb.parts);
   const double inv_n = 1.0 / (double)n;
   auto at = [&](uint32_t part, uint32_t i) { return Cx{P[(size_t)part * 2 * M + i], P[(size_t)part * 2 * M + M + i]}; };
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < M; k += gridDim.x * blockDim.x) {

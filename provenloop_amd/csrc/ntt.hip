@@ -31,11 +31,12 @@
 // wavefronts drift apart, overlapping one another's twiddle loads, arithmetic
 // and stores. Forward: bits 13..10 in the lane-contiguous load layout, the
 // workgroup exchange, then bits 9..0 in wavefront-local passes, stored from
-// the wavefront-contiguous layout. Inverse: the mirror image, with the first
-// stage's twiddles loaded before the coefficients. Passes whose twiddle
-// indices are uniform across a wavefront read them with scalar loads. The
-// fused load/store operations are template parameters, so each kernel
-// carries only its own.
+// the wavefront-contiguous layout. Inverse: the mirror image. Passes whose
+// twiddle indices are uniform across a wavefront read them with scalar loads.
+// Every other global access goes through address-space-1 pointers, so it is a
+// global_* instruction: generic (flat) accesses would also count against the
+// LDS wait counter and hold up every exchange. The fused load/store
+// operations are template parameters, so each kernel carries only its own.
 #include "ntt_arith.h"
 
 namespace th {
@@ -104,7 +105,7 @@ __device__ __forceinline__ uint32_t jhi_of(uint32_t tid) {
 // Forward stages for bits BHI down to BLO on the layout with register bits [LO, LO+LE).
 template <int LOGN, int LO, int BHI, int BLO, class A>
 __device__ __forceinline__ void fwd_pass(typename A::V (&x)[Shape<LOGN>::E], uint32_t tid,
-                                         const typename A::Tw* __restrict__ tw, const A& ar) {
+                                         GPtr<typename A::Tw> tw, const A& ar) {
   using S = Shape<LOGN>;
   const uint32_t jhi = jhi_of<LOGN, LO>(tid);
 #pragma unroll
@@ -115,18 +116,16 @@ __device__ __forceinline__ void fwd_pass(typename A::V (&x)[Shape<LOGN>::E], uin
     for (int k = 0; k < S::E; ++k) {
       if (k & (1 << rb)) continue;
       const int k2 = k | (1 << rb);
-      const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+      const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
       ar.fwd(x[k], x[k2], t);
     }
   }
 }
 
-// Inverse stages for bits BLO up to BHI. `pre` (may be null) holds the twiddles
-// of stage BLO, loaded ahead of time.
+// Inverse stages for bits BLO up to BHI.
 template <int LOGN, int LO, int BLO, int BHI, class A>
 __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uint32_t tid,
-                                         const typename A::Tw* __restrict__ tw, const A& ar,
-                                         const LimbConst& lc, const typename A::Tw* pre) {
+                                         GPtr<typename A::Tw> tw, const A& ar, const LimbConst& lc) {
   using S = Shape<LOGN>;
   const uint32_t jhi = jhi_of<LOGN, LO>(tid);
 #pragma unroll
@@ -140,9 +139,7 @@ __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uin
       if (b == LOGN - 1) {
         ar.inv_last(x[k], x[k2], lc);
       } else {
-        const uint32_t m = (uint32_t)(k >> (rb + 1));
-        const typename A::Tw t = (pre && b == BLO) ? pre[m] : tw[base | m];
-        ar.inv(x[k], x[k2], t);
+        ar.inv(x[k], x[k2], ld16(tw, base | (uint32_t)(k >> (rb + 1))));
       }
     }
   }
@@ -157,7 +154,7 @@ __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uin
 // wavefront, so after the first exchange the wavefronts run without barriers.
 template <int LOGN, int TOP, int CUR_LO, class A>
 __device__ __forceinline__ void fwd_passes(typename A::V (&x)[Shape<LOGN>::E], typename A::V* lds,
-                                           uint32_t tid, const typename A::Tw* tw, const A& ar) {
+                                           uint32_t tid, GPtr<typename A::Tw> tw, const A& ar) {
   using S = Shape<LOGN>;
   if constexpr (TOP > 0) {
     constexpr int LO = TOP - S::LE > 0 ? TOP - S::LE : 0;
@@ -196,14 +193,14 @@ constexpr int inv_end_lo() {
 // Remaining inverse passes: bits [BOT .. LOGN-1] still to do.
 template <int LOGN, int BOT, int CUR_LO, class A>
 __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], typename A::V* lds,
-                                           uint32_t tid, const typename A::Tw* tw, const A& ar,
-                                           const LimbConst& lc, const typename A::Tw* pre) {
+                                           uint32_t tid, GPtr<typename A::Tw> tw, const A& ar,
+                                           const LimbConst& lc) {
   if constexpr (BOT < LOGN) {
     constexpr int LO = inv_lo<LOGN>(BOT);
     constexpr int HI = inv_hi<LOGN>(BOT);
     if constexpr (LO != CUR_LO) exchange<LOGN, CUR_LO, LO>(x, lds, tid);
-    inv_pass<LOGN, LO, BOT, HI, A>(x, tid, tw, ar, lc, pre);
-    inv_passes<LOGN, HI + 1, LO, A>(x, lds, tid, tw, ar, lc, nullptr);
+    inv_pass<LOGN, LO, BOT, HI, A>(x, tid, tw, ar, lc);
+    inv_passes<LOGN, HI + 1, LO, A>(x, lds, tid, tw, ar, lc);
   }
 }
 
@@ -213,35 +210,27 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
   using S = Shape<LOGN>;
   const uint32_t tid = threadIdx.x;
   const A ar(lc);
+  const GMut<uint64_t> gdst = gst(dst);
   typename A::V x[S::E];
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
 #pragma unroll
     for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, S::COAL_LO>(tid, k)));
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
     fwd_passes<LOGN, LOGN, S::COAL_LO, A>(x, lds, tid, tw, ar);
 #pragma unroll
     for (int k = 0; k < S::E; ++k) {
       const uint32_t i = elem<S::LE, S::WAVE_LO>(tid, k);
-      dst[i] = so(ar.fwd_store(x[k]), i);
+      gdst[i] = so(ar.fwd_store(x[k]), i);
     }
   } else {
-    // the first pass (layout LO = 0, bits 0..3) needs the most distinct
-    // twiddles; its first stage's 8 are loaded before the coefficients so
-    // that their latency hides behind the coefficient loads
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
-    typename A::Tw pre[S::E / 2];
-    {
-      const uint32_t base = ((uint32_t)S::N | (tid << S::LE)) >> 1;
-#pragma unroll
-      for (int m = 0; m < S::E / 2; ++m) pre[m] = tw[base | (uint32_t)m];
-    }
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
 #pragma unroll
     for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, S::WAVE_LO>(tid, k)));
-    inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, tw, ar, lc, pre);
+    inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, tw, ar, lc);
     constexpr int END = inv_end_lo<LOGN>();
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) dst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
+    for (int k = 0; k < S::E; ++k) gdst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
   }
 }
 
@@ -276,7 +265,7 @@ template <int LOGN, bool INV>
 static hipError_t launch_one(const NttArgs& a, uint32_t njobs, hipStream_t s) {
   using S = Shape<LOGN>;
   const size_t lds = (size_t)S::LDS_ELEMS * 8;
-  return with_ops(INV, a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
+  return with_ops<INV>(a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
                   [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
                     static bool attr_set = false;  // one per instantiation
                     if (!attr_set) {

@@ -91,11 +91,11 @@ struct LoadOp {
   const uint64_t* key;  // secret-key limb-poly (DOT)
   BarrettConst bc;
   RescaleConst rc;
-  __device__ __forceinline__ uint64_t operator()(const uint64_t* __restrict__ src, uint32_t i) const {
-    const uint64_t x = src[i];
-    if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, aux[i], bc);
+  __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
+    const uint64_t x = gld(src)[i];
+    if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
     if constexpr (LD == NTT_LOAD_REDUCE) return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
-    if constexpr (LD == NTT_LOAD_DOT) return addmod(x, mulmod_barrett(aux[i], key[i], bc), bc.q);
+    if constexpr (LD == NTT_LOAD_DOT) return addmod(x, mulmod_barrett(gld(aux)[i], gld(key)[i], bc), bc.q);
     return x;
   }
 };
@@ -113,9 +113,9 @@ struct StoreOp {
     } else {
       uint64_t c;
       if constexpr (ST == NTT_STORE_MUL_RESCALE)
-        c = mulmod_barrett(aux[i], aux2[i], bc);
+        c = mulmod_barrett(gld(aux)[i], gld(aux2)[i], bc);
       else
-        c = aux[i];
+        c = gld(aux)[i];
       return csub(shoup_lazy(submod(c, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
     }
   }
@@ -138,21 +138,22 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE, NONE),
 // (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT, NONE).
-template <class F>
-__host__ hipError_t with_ops(bool inverse, uint32_t load, uint32_t store, F&& f) {
-  if (!inverse) {
+template <bool INV, class F>
+__host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
+  if constexpr (!INV) {
     if (load == NTT_LOAD_NONE && store == NTT_STORE_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_RESCALE)
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_RESCALE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_MUL_RESCALE)
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_MUL_RESCALE>();
     return hipErrorInvalidValue;
+  } else {
+    if (store != NTT_STORE_NONE) return hipErrorInvalidValue;
+    if (load == NTT_LOAD_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_DOT) return f.template operator()<NTT_LOAD_DOT, NTT_STORE_NONE>();
+    return hipErrorInvalidValue;
   }
-  if (store != NTT_STORE_NONE) return hipErrorInvalidValue;
-  if (load == NTT_LOAD_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
-  if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();
-  if (load == NTT_LOAD_DOT) return f.template operator()<NTT_LOAD_DOT, NTT_STORE_NONE>();
-  return hipErrorInvalidValue;
 }
 
 }  // namespace th

@@ -59,7 +59,7 @@ __device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
 // Forward stages BHI down to BLO on registers that hold index bits
 // [EB, EB + 4); f = index of register 0 (its register bits are zero).
 template <int LOGN, int EB, int BHI, int BLO, class A>
-__device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, const typename A::Tw* __restrict__ tw,
+__device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar) {
 #pragma unroll
   for (int b = BHI; b >= BLO; --b) {
@@ -68,7 +68,7 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, c
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k & (1 << rb)) continue;
-      const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+      const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
       ar.fwd(x[k], x[k | (1 << rb)], t);
     }
   }
@@ -76,7 +76,7 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, c
 
 // Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
 template <int LOGN, int EB, int BLO, int BHI, class A>
-__device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, const typename A::Tw* __restrict__ tw,
+__device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar, const LimbConst& lc) {
 #pragma unroll
   for (int b = BLO; b <= BHI; ++b) {
@@ -88,7 +88,7 @@ __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, c
       if (b == LOGN - 1) {
         ar.inv_last(x[k], x[k | (1 << rb)], lc);
       } else {
-        const typename A::Tw t = tw[base | (uint32_t)(k >> (rb + 1))];
+        const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
         ar.inv(x[k], x[k | (1 << rb)], t);
       }
     }
@@ -127,26 +127,27 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
   auto e1 = [&](uint32_t k) { return (row1(k) << WL) | lcol; };
   auto e2 = [&](uint32_t k) { return (row2(k) << WL) | lcol; };
   const A ar(lc);
+  const GMut<uint64_t> gdst = gst(dst);
   typename A::V x[16];
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
 #pragma unroll
     for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, (row1(k) << CB) | col));
     fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4>(x, (row1(0) << CB) | col, tw, ar);
     wave_exchange(x, lds, e1, e2);
     fwd_stages<LOGN, CB, LOGN - 5, CB>(x, (row2(0) << CB) | col, tw, ar);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) dst[(row2(k) << CB) | col] = ar.raw(x[k]);
+    for (int k = 0; k < 16; ++k) gdst[(row2(k) << CB) | col] = ar.raw(x[k]);
   } else {
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(dst[(row2(k) << CB) | col]);
+    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gdst[(row2(k) << CB) | col]);
     inv_stages<LOGN, CB, CB, CB + 3>(x, (row2(0) << CB) | col, tw, ar, lc);
     wave_exchange(x, lds, e2, e1);
     inv_stages<LOGN, LOGN - 4, CB + 4, LOGN - 1>(x, (row1(0) << CB) | col, tw, ar, lc);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) dst[(row1(k) << CB) | col] = ar.inv_store(x[k]);
+    for (int k = 0; k < 16; ++k) gdst[(row1(k) << CB) | col] = ar.inv_store(x[k]);
   }
 }
 
@@ -164,20 +165,21 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
   auto p2 = [&](uint32_t k) { return k | ((l & M) << 4) | rowbits; };
   auto g = [&](uint32_t k) { return l + 64 * k; };
   const A ar(lc);
+  const GMut<uint64_t> gdst = gst(dst);
   typename A::V x[16];
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.fwd);
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(dst[jbase + p1(k)]);
+    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gdst[jbase + p1(k)]);
     fwd_stages<LOGN, CB - 4, CB - 1, CB - 4>(x, jbase + p1(0), tw, ar);
     wave_exchange(x, lds, p1, p2);
     fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
     wave_exchange(x, lds, p2, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) dst[jbase + g(k)] = so(ar.fwd_store(x[k]), jbase + g(k));
+    for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so(ar.fwd_store(x[k]), jbase + g(k));
   } else {
-    const typename A::Tw* tw = reinterpret_cast<const typename A::Tw*>(lc.inv);
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
 #pragma unroll
     for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
     wave_exchange(x, lds, g, p2);
@@ -185,7 +187,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     wave_exchange(x, lds, p2, p1);
     inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) dst[jbase + p1(k)] = ar.raw(x[k]);
+    for (int k = 0; k < 16; ++k) gdst[jbase + p1(k)] = ar.raw(x[k]);
   }
 }
 
@@ -239,29 +241,32 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
 // The pass that reads the transform's input (column pass forward, row pass
 // inverse) carries the load operation, the forward row pass the store
 // operation; the other pass is instantiated with none.
-template <int LOGN>
-static hipError_t launch_split_t(bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
+template <int LOGN, bool INV>
+static hipError_t launch_split_t(const NttArgs& a, uint32_t njobs, hipStream_t s) {
   using S = Split<LOGN>;
   const dim3 grid(njobs * S::PARTS), block(64);
-  return with_ops(inverse, a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
-                  [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
-                    if (!inverse) {
-                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, LD, NTT_STORE_NONE>), grid, block, 0, s, a);
-                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false, NTT_LOAD_NONE, ST>), grid, block, 0, s, a);
-                    } else {
-                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, LD, NTT_STORE_NONE>), grid, block, 0, s, a);
-                      hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, true, NTT_LOAD_NONE, NTT_STORE_NONE>), grid, block,
-                                         0, s, a);
-                    }
-                    return hipGetLastError();
-                  });
+  return with_ops<INV>(a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
+                       [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+                         if constexpr (!INV) {
+                           hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, LD, NTT_STORE_NONE>), grid, block,
+                                              0, s, a);
+                           hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false, NTT_LOAD_NONE, ST>), grid, block,
+                                              0, s, a);
+                         } else {
+                           hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, LD, NTT_STORE_NONE>), grid, block,
+                                              0, s, a);
+                           hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, true, NTT_LOAD_NONE, NTT_STORE_NONE>), grid,
+                                              block, 0, s, a);
+                         }
+                         return hipGetLastError();
+                       });
 }
 
 hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
   switch (logn) {
-    case 13: return launch_split_t<13>(inverse, a, njobs, s);
-    case 14: return launch_split_t<14>(inverse, a, njobs, s);
-    case 15: return launch_split_t<15>(inverse, a, njobs, s);
+    case 13: return inverse ? launch_split_t<13, true>(a, njobs, s) : launch_split_t<13, false>(a, njobs, s);
+    case 14: return inverse ? launch_split_t<14, true>(a, njobs, s) : launch_split_t<14, false>(a, njobs, s);
+    case 15: return inverse ? launch_split_t<15, true>(a, njobs, s) : launch_split_t<15, false>(a, njobs, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -25,8 +25,8 @@ __global__ void k_ct_pt_mul(const CtPtJob* __restrict__ jobs, const BarrettConst
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < 2 * per_comp; e += gridDim.x * blockDim.x) {
     const uint32_t w = e < per_comp ? e : e - per_comp;
     const uint32_t l = w / n;
-    const uint64_t c = (e < per_comp ? jb.ct0 : jb.ct1)[w];
-    jb.out[e] = mulmod_barrett(c, jb.pt[w], bc[l]);
+    const uint64_t c = gld(e < per_comp ? jb.ct0 : jb.ct1)[w];
+    gst(jb.out)[e] = mulmod_barrett(c, gld(jb.pt)[w], bc[l]);
   }
 }
 
@@ -37,7 +37,8 @@ __global__ void k_ct_addsub(const AddJob* __restrict__ jobs, const uint64_t* __r
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
     const uint32_t l = (e / n) % jb.limbs;
     const uint64_t m = q[l];
-    jb.out[e] = jb.sub ? submod(jb.a[e], jb.b[e], m) : addmod(jb.a[e], jb.b[e], m);
+    const uint64_t a = gld(jb.a)[e], b = gld(jb.b)[e];
+    gst(jb.out)[e] = jb.sub ? submod(a, b, m) : addmod(a, b, m);
   }
 }
 
@@ -92,11 +93,12 @@ __global__ void k_encrypt_combine(const EncCombineJob* __restrict__ jobs, const 
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
     const uint32_t l = e / n;
     const BarrettConst m = bc[l];
-    const uint64_t U = jb.prep[2 * total + e];
-    const uint64_t bu = mulmod_barrett(jb.pk_b[e], U, m);
-    const uint64_t au = mulmod_barrett(jb.pk_a[e], U, m);
-    jb.out[e] = addmod(bu, jb.prep[e], m.q);
-    jb.out[total + e] = addmod(au, jb.prep[total + e], m.q);
+    const GPtr<uint64_t> prep = gld(jb.prep);
+    const uint64_t U = prep[2 * total + e];
+    const uint64_t bu = mulmod_barrett(gld(jb.pk_b)[e], U, m);
+    const uint64_t au = mulmod_barrett(gld(jb.pk_a)[e], U, m);
+    gst(jb.out)[e] = addmod(bu, prep[e], m.q);
+    gst(jb.out)[total + e] = addmod(au, prep[total + e], m.q);
   }
 }
 

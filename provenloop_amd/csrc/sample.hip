@@ -89,7 +89,7 @@ __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, 
     bool zero = false;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      jb.u[16 * b + i] = ternary_value(w[i]);
+      gst(jb.u)[16 * b + i] = ternary_value(w[i]);
       zero |= w[i] == 0;
     }
     if (zero && jb.reject) atomicOr(jb.reject, 1u);  // range_u32 rejects 0 (rng.rs:112-119)
@@ -100,9 +100,9 @@ __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, 
       const uint32_t g = g0 + t;
       const int64_t e = gaussian_rounded(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3]);
       if (g < n)
-        jb.e0[g] = e;
+        gst(jb.e0)[g] = e;
       else
-        jb.e1[g - n] = e;
+        gst(jb.e1)[g - n] = e;
     }
   }
 }

@@ -53,6 +53,32 @@ __device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t 
 
 __device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t m) { return x >= m ? x - m : x; }
 
+// Pointers known to address global memory (address space 1). Pointers read
+// from job descriptors or constant tables are generic to the compiler, and
+// generic (flat) loads and stores also count against the LDS wait counter,
+// which serialises them with every LDS exchange; accesses through these
+// pointers are global_* instructions instead.
+template <class T>
+using GPtr = const __attribute__((address_space(1))) T*;
+template <class T>
+using GMut = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ GPtr<T> gld(const T* p) {
+  return (GPtr<T>)p;
+}
+template <class T>
+__device__ __forceinline__ GMut<T> gst(T* p) {
+  return (GMut<T>)p;
+}
+// Element i of a global array of 16-byte records (twiddle pairs), loaded as one
+// 16-byte vector.
+template <class T>
+__device__ __forceinline__ T ld16(GPtr<T> p, uint32_t i) {
+  static_assert(sizeof(T) == 16, "16-byte records only");
+  using V = uint64_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(T, ((GPtr<V>)p)[i]);
+}
+
 // floor(x * s / 2^64) - e with e in {0, 1, 2}: x1*s1 + hi(x1*s0) + hi(x0*s1)
 // for 32-bit halves; the low halves of the two cross products and hi(x0*s0)
 // are dropped, each below 2^32, so at most 2 is lost after the shift.
