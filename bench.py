@@ -160,6 +160,22 @@ def ntt_roofline(ctx, reps=20):
     }
 
 
+def ntt_traffic():
+    """HBM bytes per launch of the batched NTT (mean of forward and inverse),
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of
+    `bench.py --ntt-only`, scaled by the calibration copy's factor; None if
+    the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "ntt_64x4_n16384_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            p = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = p["calibration"]["factor"]
+    per = [(p[d]["fetch_kib"] + p[d]["write_kib"]) * 1024 * k for d in ("forward", "inverse")]
+    return int(sum(per) / len(per))
+
+
 # ------------------------------------------------------------------ CPU oracle side
 class CpuLayer:
     """One layer of the per-token pass on the CPU oracle (checker / baseline only)."""
@@ -584,7 +600,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(ntt["roundtrip_GBs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": ntt_traffic(),
         },
         "pipelined": {
             "value": round(deltas_per_token * args.steps / piped, 3), "unit": "deltas/s",
