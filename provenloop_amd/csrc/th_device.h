@@ -91,8 +91,17 @@ __device__ __forceinline__ uint64_t mulhi_approx(uint64_t x, uint64_t s) {
 // x * w mod q in [0, 4q) for any 64-bit x (w < q, ws = floor(w * 2^64 / q)):
 // the exact Shoup remainder is below 2q and the quotient estimate is at most
 // 2 short.
+// The remainder is formed as x*w + qhat*(2^64 - q) mod 2^64 from 32-bit
+// partial products, so that the second low product accumulates onto the first
+// (one multiply-add) instead of being subtracted as a separate 64-bit word.
 __device__ __forceinline__ uint64_t shoup_approx(uint64_t x, uint64_t w, uint64_t ws, uint64_t q) {
-  return x * w - mulhi_approx(x, ws) * q;
+  const uint64_t qh = mulhi_approx(x, ws);
+  const uint64_t nq = 0 - q;
+  const uint32_t x0 = (uint32_t)x, x1 = (uint32_t)(x >> 32), w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+  const uint32_t h0 = (uint32_t)qh, h1 = (uint32_t)(qh >> 32), n0 = (uint32_t)nq, n1 = (uint32_t)(nq >> 32);
+  const uint64_t lo = (uint64_t)x0 * w0 + (uint64_t)h0 * n0;
+  const uint32_t hi = (uint32_t)(lo >> 32) + x0 * w1 + x1 * w0 + h0 * n1 + h1 * n0;
+  return ((uint64_t)hi << 32) | (uint32_t)lo;
 }
 
 // Exact a*b mod q for a, b < q < 2^63 (operands without a precomputed
