@@ -22,10 +22,13 @@ struct IntArith {
   using Tw = ShoupTw;
   uint64_t q, two_q, four_q;
   __device__ IntArith(const LimbConst& c) : q(c.q), two_q(c.two_q), four_q(2 * c.two_q) {}
+  // 2^64 - 4q, the forward butterfly's csub_n addend (the same value at every
+  // call, so the compiler keeps one copy)
+  __device__ __forceinline__ uint64_t n4q() const { return opaque_u64(0 - four_q); }
   __device__ __forceinline__ V load(uint64_t x) const { return x; }
   // forward CT butterfly, inputs/outputs in [0, 8q): X < 4q, T < 4q
   __device__ __forceinline__ void fwd(V& a, V& b, const Tw& t) const {
-    const uint64_t X = csub(a, four_q);
+    const uint64_t X = csub_n(a, four_q, n4q());
     const uint64_t T = shoup_approx(b, t.w, t.ws, q);
     a = X + T;
     b = X + four_q - T;
@@ -43,7 +46,7 @@ struct IntArith {
     b = csub(csub(shoup_approx(X + four_q - Y, c.last_w, c.last_ws, q), two_q), q);
   }
   __device__ __forceinline__ void inv_pass_end(V&) const {}
-  __device__ __forceinline__ uint64_t fwd_store(V x) const { return csub(csub(csub(x, four_q), two_q), q); }
+  __device__ __forceinline__ uint64_t fwd_store(V x) const { return csub(csub(csub_n(x, four_q, n4q()), two_q), q); }
   __device__ __forceinline__ uint64_t inv_store(V x) const { return x; }
   __device__ __forceinline__ uint64_t raw(V x) const { return x; }
   __device__ __forceinline__ V unraw(uint64_t x) const { return x; }

@@ -53,6 +53,21 @@ __device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t 
 
 __device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t m) { return x >= m ? x - m : x; }
 
+// The same with nm = 2^64 - m supplied: x + nm is one 64-bit add (no borrow
+// chain through VCC), and the compare selects between x and the sum.
+__device__ __forceinline__ uint64_t csub_n(uint64_t x, uint64_t m, uint64_t nm) {
+  const uint64_t t = x + nm;
+  return x >= m ? t : x;
+}
+
+// v unchanged, but hidden from the optimiser (an empty asm that claims to
+// modify it), so that 2^64 - m stays an addend instead of being folded back
+// into a subtraction of m.
+__device__ __forceinline__ uint64_t opaque_u64(uint64_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 // Pointers known to address global memory (address space 1). Pointers read
 // from job descriptors or constant tables are generic to the compiler, and
 // generic (flat) loads and stores also count against the LDS wait counter,
