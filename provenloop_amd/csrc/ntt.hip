@@ -47,6 +47,8 @@ constexpr int NTT_WHOLE_MAX_LOGN = 14;
 #define NTT_WHOLE_MAX_JOBS 256
 #endif
 hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
+hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf,
+                                hipStream_t s);
 
 template <int LOGN>
 struct Shape {
@@ -279,10 +281,24 @@ static hipError_t launch_one(const NttArgs& a, uint32_t njobs, hipStream_t s) {
                   });
 }
 
+static bool use_split(int logn, uint32_t njobs) {
+  return logn >= NTT_SPLIT_MIN_LOGN && (logn > NTT_WHOLE_MAX_LOGN || njobs > NTT_WHOLE_MAX_JOBS);
+}
+
+hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nfwd,
+                          hipStream_t s) {
+  if (ninv == 0) return hipSuccess;
+  if (use_split(logn, nfwd) && inv.jobs && fwd.jobs && nfwd % ninv == 0 && inv.store == NTT_STORE_NONE &&
+      fwd.load == NTT_LOAD_REDUCE)
+    return launch_rescale_split(logn, inv, ninv, fwd, nfwd / ninv, s);
+  hipError_t e = launch_ntt(logn, true, inv, ninv, s);
+  if (e != hipSuccess) return e;
+  return launch_ntt(logn, false, fwd, nfwd, s);
+}
+
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
   if (njobs == 0) return hipSuccess;
-  if (logn >= NTT_SPLIT_MIN_LOGN && (logn > NTT_WHOLE_MAX_LOGN || njobs > NTT_WHOLE_MAX_JOBS))
-    return launch_ntt_split(logn, inverse, a, njobs, s);
+  if (use_split(logn, njobs)) return launch_ntt_split(logn, inverse, a, njobs, s);
 #define TH_NTT_CASE(L) \
   case L: return inverse ? launch_one<L, true>(a, njobs, s) : launch_one<L, false>(a, njobs, s);
   switch (logn) {

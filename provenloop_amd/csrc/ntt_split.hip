@@ -113,41 +113,74 @@ __device__ __forceinline__ void wave_exchange(V (&x)[16], V* lds, From from, To 
 }
 
 // ------------------------------------------------------------------ column pass
+// Column geometry of wavefront `part`: CW adjacent columns, all 2^RB rows.
+template <int LOGN>
+struct ColumnMap {
+  using S = Split<LOGN>;
+  static constexpr int RB = S::RB, CB = S::CB, CW = S::CW, WL = 10 - RB;  // WL = log2(CW)
+  uint32_t lcol, lrow, col;
+  __device__ explicit ColumnMap(uint32_t part) {
+    const uint32_t l = threadIdx.x;
+    lcol = l & (CW - 1);
+    lrow = l >> WL;
+    col = part * CW + lcol;
+  }
+  // Q1 and Q2 element maps: local e = (row << WL) | lcol, global j = (row << CB) | col
+  __device__ uint32_t row1(uint32_t k) const { return lrow | (k << (RB - 4)); }
+  __device__ uint32_t row2(uint32_t k) const { return k | (lrow << 4); }
+  __device__ uint32_t e1(uint32_t k) const { return (row1(k) << WL) | lcol; }
+  __device__ uint32_t e2(uint32_t k) const { return (row2(k) << WL) | lcol; }
+  __device__ uint32_t j1(uint32_t k) const { return (row1(k) << CB) | col; }
+  __device__ uint32_t j2(uint32_t k) const { return (row2(k) << CB) | col; }
+};
+
+// Forward column pass on coefficients already in registers (Q1 layout, the
+// arithmetic's representation); writes the intermediate to dst (Q2).
+template <int LOGN, class A>
+__device__ __forceinline__ void column_fwd_regs(typename A::V (&x)[16], uint64_t* dst, const LimbConst& lc,
+                                                const ColumnMap<LOGN>& m, const A& ar, uint64_t* lds_raw) {
+  constexpr int CB = Split<LOGN>::CB;
+  const GMut<uint64_t> gdst = gst(dst);
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
+  fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4>(x, m.j1(0), tw, ar);
+  wave_exchange(x, lds, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
+  fwd_stages<LOGN, CB, LOGN - 5, CB>(x, m.j2(0), tw, ar);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) gdst[m.j2(k)] = ar.raw(x[k]);
+}
+
+// Inverse column pass from the row pass's intermediate in buf (Q2); leaves
+// the transform's final values in registers (Q1 layout).
+template <int LOGN, class A>
+__device__ __forceinline__ void column_inv_regs(typename A::V (&x)[16], const uint64_t* buf, const LimbConst& lc,
+                                                const ColumnMap<LOGN>& m, const A& ar, uint64_t* lds_raw) {
+  constexpr int CB = Split<LOGN>::CB;
+  const GPtr<uint64_t> gbuf = gld(buf);
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gbuf[m.j2(k)]);
+  inv_stages<LOGN, CB, CB, CB + 3>(x, m.j2(0), tw, ar, lc);
+  wave_exchange(x, lds, [&](uint32_t k) { return m.e2(k); }, [&](uint32_t k) { return m.e1(k); });
+  inv_stages<LOGN, LOGN - 4, CB + 4, LOGN - 1>(x, m.j1(0), tw, ar, lc);
+}
+
 template <int LOGN, bool INV, class A, class LOp>
 __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
                                             const LimbConst& lc, const LOp& op, uint32_t part, uint64_t* lds_raw) {
-  using S = Split<LOGN>;
-  constexpr int RB = S::RB, CB = S::CB, CW = S::CW, WL = 10 - RB;  // WL = log2(CW)
-  const uint32_t l = threadIdx.x;
-  const uint32_t lcol = l & (CW - 1), lrow = l >> WL;
-  const uint32_t col = part * CW + lcol;
-  // Q1 and Q2 element maps: local e = (row << WL) | lcol, global j = (row << CB) | col
-  auto row1 = [&](uint32_t k) { return lrow | (k << (RB - 4)); };
-  auto row2 = [&](uint32_t k) { return k | (lrow << 4); };
-  auto e1 = [&](uint32_t k) { return (row1(k) << WL) | lcol; };
-  auto e2 = [&](uint32_t k) { return (row2(k) << WL) | lcol; };
+  const ColumnMap<LOGN> m(part);
   const A ar(lc);
-  const GMut<uint64_t> gdst = gst(dst);
   typename A::V x[16];
-  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   if constexpr (!INV) {
-    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, (row1(k) << CB) | col));
-    fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4>(x, (row1(0) << CB) | col, tw, ar);
-    wave_exchange(x, lds, e1, e2);
-    fwd_stages<LOGN, CB, LOGN - 5, CB>(x, (row2(0) << CB) | col, tw, ar);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) gdst[(row2(k) << CB) | col] = ar.raw(x[k]);
+    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, m.j1(k)));
+    column_fwd_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
   } else {
-    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
+    column_inv_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
+    const GMut<uint64_t> gdst = gst(dst);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gdst[(row2(k) << CB) | col]);
-    inv_stages<LOGN, CB, CB, CB + 3>(x, (row2(0) << CB) | col, tw, ar, lc);
-    wave_exchange(x, lds, e2, e1);
-    inv_stages<LOGN, LOGN - 4, CB + 4, LOGN - 1>(x, (row1(0) << CB) | col, tw, ar, lc);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) gdst[(row1(k) << CB) | col] = ar.inv_store(x[k]);
+    for (int k = 0; k < 16; ++k) gdst[m.j1(k)] = ar.inv_store(x[k]);
   }
 }
 
@@ -192,6 +225,20 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
 }
 
 // ------------------------------------------------------------------ kernels
+// Column-pass part of workgroup part id p: 8-column parts share 128-byte lines
+// in pairs; ids i and i + 8 run on one XCD (ids are dealt round-robin over the
+// 8 XCDs), so they get the column parts 2m and 2m + 1.
+template <int LOGN>
+__device__ __forceinline__ uint32_t column_part(uint32_t p) {
+  using S = Split<LOGN>;
+  if constexpr (S::CW < 16) {
+    static_assert(S::CW == 8 && S::PARTS % 16 == 0, "column-part pairing needs 8 columns and 16 | PARTS");
+    return (p & ~15u) | ((p & 7u) << 1) | ((p >> 3) & 1u);
+  } else {
+    return p;
+  }
+}
+
 // Workgroup b works on part b % PARTS of job b / PARTS. The pass that reads
 // the transform's input applies the fused load operation and the forward
 // row pass the fused store operation; otherwise passes read and write the
@@ -202,12 +249,7 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   __shared__ uint64_t lds[S::LDS];
   const uint32_t job = blockIdx.x / S::PARTS;
   uint32_t part = blockIdx.x % S::PARTS;
-  if constexpr (COLUMN && S::CW < 16) {
-    // 8-column parts share 128-byte lines in pairs; ids i and i + 8 run on one
-    // XCD, so they get the column parts 2m and 2m + 1
-    static_assert(S::CW == 8 && S::PARTS % 16 == 0, "column-part pairing needs 8 columns and 16 | PARTS");
-    part = (part & ~15u) | ((part & 7u) << 1) | ((part >> 3) & 1u);
-  }
+  if constexpr (COLUMN) part = column_part<LOGN>(part);
   const uint64_t* src;
   uint64_t* dst;
   uint32_t limb;
@@ -235,6 +277,86 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
       row_pass<LOGN, INV, Fp64Arith>(src, dst, lc, op, so, part, lds);
     else
       row_pass<LOGN, INV, IntArith>(src, dst, lc, op, so, part, lds);
+  }
+}
+
+// Rescale column kernel: the column pass that ends the inverse transform of a
+// product's last limb, fused with the column passes that begin the forward
+// transforms of that limb reduced modulo each lower limb (the evaluation-
+// domain rescale), so the coefficient-domain last limb stays in registers.
+// Inverse job i (its dst holds the inverse row pass's intermediate) owns
+// forward jobs i * nf .. i * nf + nf - 1, the order in which the rescale lists
+// them; each forward job's dst receives its column-pass intermediate, where
+// the forward row pass continues (with the rescale's store operation).
+template <int LOGN>
+__global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs fwd, uint32_t nf) {
+  using S = Split<LOGN>;
+  __shared__ uint64_t lds[S::LDS];
+  const uint32_t job = blockIdx.x / S::PARTS;
+  const ColumnMap<LOGN> m(column_part<LOGN>(blockIdx.x % S::PARTS));
+  const NttJob ij = inv.jobs[job];
+  const LimbConst& lci = inv.lc[ij.limb];
+  uint64_t c[16];  // canonical last-limb coefficients of this wavefront's columns (Q1)
+  if (lci.fp64) {
+    const Fp64Arith ar(lci);
+    Fp64Arith::V x[16];
+    column_inv_regs<LOGN>(x, ij.dst, lci, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
+  } else {
+    const IntArith ar(lci);
+    IntArith::V x[16];
+    column_inv_regs<LOGN>(x, ij.dst, lci, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
+  }
+  for (uint32_t f = 0; f < nf; ++f) {
+    const NttJob fj = fwd.jobs[(uint64_t)job * nf + f];
+    const LimbConst& lcf = fwd.lc[fj.limb];
+    const RescaleConst rc = fwd.rc[fj.limb];
+    if (lcf.fp64) {
+      const Fp64Arith ar(lcf);
+      Fp64Arith::V x[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b));
+      column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
+    } else {
+      const IntArith ar(lcf);
+      IntArith::V x[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b));
+      column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
+    }
+  }
+}
+
+template <int LOGN>
+static hipError_t launch_rescale_t(const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf, hipStream_t s) {
+  using S = Split<LOGN>;
+  const dim3 block(64);
+  const hipError_t e = with_ops<true>(inv.load, inv.store, [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, LD, NTT_STORE_NONE>), dim3(ninv * S::PARTS), block, 0, s,
+                       inv);
+    return hipGetLastError();
+  });
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((rescale_column_kernel<LOGN>), dim3(ninv * S::PARTS), block, 0, s, inv, fwd, nf);
+  const hipError_t e2 = hipGetLastError();
+  if (e2 != hipSuccess) return e2;
+  return with_ops<false>(fwd.load, fwd.store, [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+    hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, false, NTT_LOAD_NONE, ST>), dim3(ninv * nf * S::PARTS), block, 0,
+                       s, fwd);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf,
+                                hipStream_t s) {
+  switch (logn) {
+    case 13: return launch_rescale_t<13>(inv, ninv, fwd, nf, s);
+    case 14: return launch_rescale_t<14>(inv, ninv, fwd, nf, s);
+    case 15: return launch_rescale_t<15>(inv, ninv, fwd, nf, s);
+    default: return hipErrorInvalidValue;
   }
 }
 

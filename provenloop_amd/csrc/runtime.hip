@@ -696,9 +696,16 @@ void queue_rescale(OpScope& sc, const std::vector<CtView>& in, uint64_t* const* 
         fwd.push_back(NttJob{lc, out[i] + (size_t)(comp * (L - 1) + l) * N, cc + (size_t)l * N,
                              pts ? pts[i] + (size_t)l * N : nullptr, l, 0});
     }
-  ntt_list(sc, true, inv, pts ? NTT_LOAD_MUL : NTT_LOAD_NONE);
-  ntt_list(sc, false, fwd, NTT_LOAD_REDUCE, c->d_rc + (size_t)L * c->L, nullptr,
-           pts ? NTT_STORE_MUL_RESCALE : NTT_STORE_RESCALE);
+  NttArgs ia{}, fa{};
+  ia.lc = fa.lc = c->d_lc;
+  ia.bc = fa.bc = c->d_bc;
+  ia.jobs = sc.up(inv);
+  ia.load = pts ? NTT_LOAD_MUL : NTT_LOAD_NONE;
+  fa.jobs = sc.up(fwd);
+  fa.load = NTT_LOAD_REDUCE;
+  fa.store = pts ? NTT_STORE_MUL_RESCALE : NTT_STORE_RESCALE;
+  fa.rc = c->d_rc + (size_t)L * c->L;
+  HIPCHK(launch_rescale((int)c->logn, ia, (uint32_t)inv.size(), fa, (uint32_t)fwd.size(), c->stream));
 }
 
 void check_decrypt_args(th_ctx* c, const th_ct* const* cts, size_t count, const th_sk* sk) {
@@ -1623,9 +1630,16 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
     if (do_rescale) {
       // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
-      launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MUL);
-      launch_jobs_ntt(ctx, false, set->d_fwd_rs, nb * 2 * (L - 1), NTT_LOAD_REDUCE, ctx->d_rc + (size_t)L * L, nullptr,
-                      NTT_STORE_MUL_RESCALE);
+      NttArgs ia{}, fa{};
+      ia.lc = fa.lc = ctx->d_lc;
+      ia.bc = fa.bc = ctx->d_bc;
+      ia.jobs = set->d_inv_mul;
+      ia.load = NTT_LOAD_MUL;
+      fa.jobs = set->d_fwd_rs;
+      fa.load = NTT_LOAD_REDUCE;
+      fa.store = NTT_STORE_MUL_RESCALE;
+      fa.rc = ctx->d_rc + (size_t)L * L;
+      HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
       launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
     } else {
       HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));

@@ -57,6 +57,14 @@ struct NttArgs {
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
+// The two transform launches of an evaluation-domain rescale: ninv inverse
+// transforms (inv, store NONE) of the products' last limbs, then nfwd forward
+// transforms (fwd, load REDUCE) of each last limb reduced modulo the lower
+// limbs, inverse job i owning forward jobs i * (nfwd / ninv) .. on. Where the
+// split kernels run, the inverse column pass and the forward column passes
+// are one kernel (the last limb's coefficients stay in registers).
+hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nfwd,
+                          hipStream_t s);
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;

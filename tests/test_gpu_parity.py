@@ -257,6 +257,37 @@ def test_rescale_batch_matches_oracle(eng16, ref16, base_ct):
         _ct_equal(eng16, ref16, res[b], ref16.rescale(ref16.ct_pt_mul(rct, pts[b])))
 
 
+@pytest.mark.parametrize("count", [48, 130])
+def test_rescale_large_batch_matches_oracle(eng16, ref16, base_ct, count):
+    """Batches whose forward transforms take the split kernels: the inverse column
+    pass and the forward column passes run as one fused kernel."""
+    ct, rct, _ = base_ct
+    rng = np.random.default_rng(count)
+    ps = [rng.normal(size=8192) * 0.02 for _ in range(3)]
+    pts = [eng16.encode_to_ntt(p) for p in ps]
+    prods = eng16.ct_pt_mul_ntt_batch([ct] * count, [pts[i % 3] for i in range(count)])
+    res = eng16.rescale_batch(prods)
+    for i in (0, 1, 2, count - 1):
+        _ct_equal(eng16, ref16, res[i], ref16.rescale(ref16.ct_pt_mul(rct, ps[i % 3])))
+
+
+def test_rescale_batch_n32768_eight_limbs():
+    """The fused rescale kernels at N=32768 on the 8-limb chain (7 forward transforms per inverse)."""
+    from provenloop_amd.params import CHAIN_N32768_L8
+
+    eng, ref = tensafe_he.CkksContext(32768, moduli=CHAIN_N32768_L8), orc.Context(32768, CHAIN_N32768_L8)
+    sk, rsk = eng.keygen(seed=5), ref.keygen(5)
+    pk, rpk = eng.keygen_public(sk, seed=6), ref.keygen_public(rsk, 6)
+    z = np.random.default_rng(7).normal(size=16384) * 0.1
+    ct, rct = eng.encrypt_pk(z, pk, seed=8), ref.encrypt_pk(z, rpk, 8)
+    ps = [np.random.default_rng(9 + i).normal(size=16384) * 0.02 for i in range(2)]
+    pts = [eng.encode_to_ntt(p) for p in ps]
+    prods = eng.ct_pt_mul_ntt_batch([ct] * 6, [pts[i % 2] for i in range(6)])
+    res = eng.rescale_batch(prods)
+    for i in (0, 5):
+        _ct_equal(eng, ref, res[i], ref.rescale(ref.ct_pt_mul(rct, ps[i % 2])))
+
+
 # ------------------------------------------------------------------ decryption
 def test_decrypt_bit_exact_both_branches(eng16, ref16, keys16, base_ct):
     sk, pk, rsk, rpk = keys16
