@@ -235,4 +235,16 @@ void segment_weights(uint32_t n, uint32_t d, uint32_t cols, double* out) {
   }
 }
 
+void segment_weight_pairs(uint32_t n, uint32_t d, double* out) {
+  const long double pi = 3.141592653589793238462643383279502884L;
+  auto ang = [&](uint64_t m) { return pi * (long double)(m % (2ull * n)) / (long double)n; };
+  out[0] = (double)d;
+  out[1] = 2.0;
+  for (uint32_t j = 1; j < n; ++j) {
+    const long double phi = ang((uint64_t)j * d);
+    out[2 * j] = (double)(sinl(phi) * cosl(phi) / sinl(ang(j)));
+    out[2 * j + 1] = (double)(2.0L * cosl(ang(2ull * j * d)));
+  }
+}
+
 }  // namespace th

@@ -62,6 +62,12 @@ void draw_gaussian(ChaChaStream& s, size_t n, int64_t* out);
 // out[c * N + j] for segment c = slots [c d, min((c + 1) d, N/2)); long
 // double evaluation with exact integer reduction of the angles.
 void segment_weights(uint32_t n, uint32_t d, uint32_t cols, double* out);
+// The same weights in recurrence form: with phi = pi j d / N, segment c's
+// weight is W_c[j] = A_j cos((2c + 1) phi), A_j = sin(phi) / sin(pi j / N),
+// so W_{c+1} = 2 cos(2 phi) W_c - W_{c-1} with W_{-1} = W_0. out[2j] = W_0[j],
+// out[2j + 1] = 2 cos(2 phi) (j = 0: d and 2). Long double, exact angle
+// reduction; n pairs.
+void segment_weight_pairs(uint32_t n, uint32_t d, double* out);
 
 struct Encoder {
   uint32_t n = 0, logn = 0;

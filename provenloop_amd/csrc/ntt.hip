@@ -231,8 +231,53 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
     for (int k = 0; k < S::E; ++k) x[k] = ar.load(op(src, elem<S::LE, S::WAVE_LO>(tid, k)));
     inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, tw, ar, lc);
     constexpr int END = inv_end_lo<LOGN>();
+    if constexpr (SOp::kind == NTT_STORE_SEGSUM) {
+      // segment sums of the centred coefficients (limb 0): per-thread partial
+      // sums, a fixed butterfly tree per wavefront, then the wavefronts' sums
+      // in order, so the result does not depend on scheduling
+      constexpr int MAXC = NTT_SEGSUM_FUSED_MAX_COLS;
+      const uint64_t q = lc.q, half = q >> 1;
+      using D2 = double __attribute__((ext_vector_type(2)));
+      const GPtr<D2> W = gld(reinterpret_cast<const D2*>(so.segw));
+      double acc[MAXC];
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) gdst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
+      for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
+#pragma unroll
+      for (int k = 0; k < S::E; ++k) {
+        const uint32_t j = elem<S::LE, END>(tid, k);
+        const uint64_t m = ar.inv_store(x[k]);
+        const double v = m > half ? -(double)(q - m) : (double)m;
+        const D2 p = W[j];  // W_0[j], 2 cos(2 phi_j)
+        double wp = p.x, wc = p.x;
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+          if (c >= (int)so.cols) break;
+          acc[c] += v * wc;
+          const double wn = p.y * wc - wp;
+          wp = wc;
+          wc = wn;
+        }
+      }
+      double* red = reinterpret_cast<double*>(lds_raw);
+      const uint32_t lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        if (c >= (int)so.cols) break;
+        double a = acc[c];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
+        if (lane == 0) red[wave * MAXC + c] = a;
+      }
+      __syncthreads();
+      if (tid < so.cols) {
+        double t = 0.0;
+        for (uint32_t w = 0; w < S::T / 64; ++w) t += red[w * MAXC + tid];
+        gst(so.seg)[tid] = t / so.scale;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < S::E; ++k) gdst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
+    }
   }
 }
 
@@ -298,6 +343,10 @@ hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const Ntt
 
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
   if (njobs == 0) return hipSuccess;
+  if (a.jobs && a.store == NTT_STORE_SEGSUM &&
+      (!inverse || use_split(logn, njobs) || logn > NTT_WHOLE_MAX_LOGN || a.cols < 1 ||
+       a.cols > NTT_SEGSUM_FUSED_MAX_COLS))
+    return hipErrorInvalidValue;  // the segment-sum epilogue exists in the whole-polynomial inverse only
   if (use_split(logn, njobs)) return launch_ntt_split(logn, inverse, a, njobs, s);
 #define TH_NTT_CASE(L) \
   case L: return inverse ? launch_one<L, true>(a, njobs, s) : launch_one<L, false>(a, njobs, s);

@@ -103,15 +103,21 @@ struct LoadOp {
   }
 };
 
-// The operation fused into a forward transform's final store (NttStore).
+// The operation fused into a forward transform's final store (NttStore), or,
+// for SEGSUM, the inverse transform's segment-sum epilogue's operands.
 template <uint32_t ST>
 struct StoreOp {
+  static constexpr uint32_t kind = ST;
   const uint64_t* aux;
   const uint64_t* aux2;
   BarrettConst bc;
   RescaleConst rc;
+  const double* segw;  // SEGSUM
+  double* seg;
+  double scale;
+  uint32_t cols;
   __device__ __forceinline__ uint64_t operator()(uint64_t y, uint32_t i) const {
-    if constexpr (ST == NTT_STORE_NONE) {
+    if constexpr (ST == NTT_STORE_NONE || ST == NTT_STORE_SEGSUM) {
       return y;
     } else {
       uint64_t c;
@@ -134,13 +140,20 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
   if constexpr (LD == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
   so.aux = jb.aux;
   so.aux2 = jb.aux2;
-  if constexpr (ST != NTT_STORE_NONE) so.rc = a.rc[limb];
+  if constexpr (ST == NTT_STORE_RESCALE || ST == NTT_STORE_MUL_RESCALE) so.rc = a.rc[limb];
   if constexpr (ST == NTT_STORE_MUL_RESCALE) so.bc = a.bc[limb];
+  if constexpr (ST == NTT_STORE_SEGSUM) {
+    so.segw = a.segw;
+    so.seg = reinterpret_cast<double*>(jb.dst);
+    so.scale = jb.scale;
+    so.cols = a.cols;
+  }
 }
 
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE, NONE),
-// (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT, NONE).
+// (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT, NONE),
+// (DOT, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   if constexpr (!INV) {
@@ -151,6 +164,8 @@ __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_MUL_RESCALE>();
     return hipErrorInvalidValue;
   } else {
+    if (load == NTT_LOAD_DOT && store == NTT_STORE_SEGSUM)
+      return f.template operator()<NTT_LOAD_DOT, NTT_STORE_SEGSUM>();
     if (store != NTT_STORE_NONE) return hipErrorInvalidValue;
     if (load == NTT_LOAD_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
     if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();

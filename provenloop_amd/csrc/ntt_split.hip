@@ -335,6 +335,7 @@ static hipError_t launch_rescale_t(const NttArgs& inv, uint32_t ninv, const NttA
   using S = Split<LOGN>;
   const dim3 block(64);
   const hipError_t e = with_ops<true>(inv.load, inv.store, [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+    if constexpr (ST != NTT_STORE_NONE) return hipErrorInvalidValue;  // segment sums: whole kernel only
     hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, LD, NTT_STORE_NONE>), dim3(ninv * S::PARTS), block, 0, s,
                        inv);
     return hipGetLastError();
@@ -369,6 +370,7 @@ static hipError_t launch_split_t(const NttArgs& a, uint32_t njobs, hipStream_t s
   const dim3 grid(njobs * S::PARTS), block(64);
   return with_ops<INV>(a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
                        [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
+                         if constexpr (ST == NTT_STORE_SEGSUM) return hipErrorInvalidValue;  // whole kernel only
                          if constexpr (!INV) {
                            hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, LD, NTT_STORE_NONE>), grid, block,
                                               0, s, a);

@@ -86,7 +86,7 @@ size_t decode_parts_doubles(uint32_t logn);  // scratch doubles per job
 // coefficients with segment weights W (cols x N, segment_weights()); each
 // job's `seg` receives cols sums, within rounding of decode-then-sum. Uses
 // the first 16 * cols doubles of each job's `parts` as scratch.
-constexpr uint32_t SEGSUM_MAX_COLS = 16;
+constexpr uint32_t SEGSUM_MAX_COLS = NTT_SEGSUM_MAX_COLS;
 hipError_t launch_segsum(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* W,
                          uint32_t logn, uint32_t cols, hipStream_t s);
 

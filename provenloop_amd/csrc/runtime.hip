@@ -172,6 +172,7 @@ struct th_ctx {
   DevicePool pool;
   StagingRing ring;
   std::map<std::pair<uint32_t, uint32_t>, double*> seg_w;  // segment-sum weights by (d, cols)
+  std::map<uint32_t, double*> seg_p;                        // recurrence-form weight pairs by d
   std::mutex mu;
 };
 
@@ -218,11 +219,13 @@ struct th_lora {
   const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
   const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr, *d_dot_n = nullptr;
+  const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
   const CtPtJob* d_ctpt = nullptr;
   const LoraBJob* d_bjobs = nullptr;
   uint32_t dot_n_jobs = 0, dot_r_jobs = 0;
   const double* seg_w = nullptr;  // segment weights, or null: decode the slots and sum them
+  const double* seg_p = nullptr;  // the same in recurrence form (decrypt transform's epilogue)
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
     owned.push_back(p);
@@ -456,6 +459,7 @@ void destroy_ctx(th_ctx* c) {
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
+  for (auto& kv : c->seg_p) (void)hipFree(kv.second);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -617,12 +621,47 @@ const double* seg_weights(th_ctx* c, uint32_t d, uint32_t cols) {
   return dev;
 }
 
+// Segment-weight pairs (segment_weight_pairs) for segments of d slots, cached
+// per context; used by the decrypt transform's segment-sum epilogue.
+const double* seg_pairs(th_ctx* c, uint32_t d) {
+  auto it = c->seg_p.find(d);
+  if (it != c->seg_p.end()) return it->second;
+  std::vector<double> w((size_t)2 * c->N);
+  segment_weight_pairs(c->N, d, w.data());
+  double* dev = nullptr;
+  HIPCHK(hipMalloc(&dev, w.size() * 8));
+  c->seg_p[d] = dev;
+  HIPCHK(hipMemcpy(dev, w.data(), w.size() * 8, hipMemcpyHostToDevice));
+  return dev;
+}
+
 // Queue decrypt + decode of the views; slots to out_dev (count x S) and/or
 // segment sums to seg_dev (count x cols). m_l = c0_l + c1_l * s_l
 // (ciphertext.rs:332-341) is formed inside the inverse transform's load.
 // When only segment sums are wanted (and cols <= SEGSUM_MAX_COLS) they come
 // from the coefficients and the segment weights, without forming the slots.
 // Scratch lives in the caller's scope.
+// The decrypt transform can produce segment sums itself (NTT_STORE_SEGSUM)
+// when its batch runs in the whole-polynomial kernel.
+bool segsum_in_transform(const th_ctx* c, uint32_t jobs, uint32_t cols) {
+  return c->logn <= 14 && jobs <= 256 && cols >= 1 && cols <= NTT_SEGSUM_FUSED_MAX_COLS;
+}
+
+// Decrypt transforms (c0 + c1 s on limb 0, inverse NTT) whose epilogue writes
+// each job's segment sums to its dst.
+void launch_dot_segsum(th_ctx* c, const NttJob* d_jobs, uint32_t n, const th_sk* sk, const double* W, uint32_t cols) {
+  NttArgs a{};
+  a.lc = c->d_lc;
+  a.jobs = d_jobs;
+  a.load = NTT_LOAD_DOT;
+  a.store = NTT_STORE_SEGSUM;
+  a.bc = c->d_bc;
+  a.key = sk->d;
+  a.segw = W;
+  a.cols = cols;
+  HIPCHK(launch_ntt((int)c->logn, true, a, n, c->stream));
+}
+
 void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk, double* out_dev, double* seg_dev,
                    uint32_t d, uint32_t cols) {
   th_ctx* c = sc.c;
@@ -646,8 +685,19 @@ void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk,
     dec[i].scale = ct.scale;
     dec[i].crt = nl == 2;
   }
+  const bool seg_only = seg_dev && !out_dev && cols >= 1 && cols <= SEGSUM_MAX_COLS;
+  if (seg_only && nj.size() == count && segsum_in_transform(c, (uint32_t)count, cols)) {
+    // every ciphertext takes the limb-0 branch: the segment sums come out of
+    // the decrypt transform itself
+    for (size_t i = 0; i < count; ++i) {
+      nj[i].dst = reinterpret_cast<uint64_t*>(seg_dev + i * cols);
+      nj[i].scale = cts[i].scale;
+    }
+    launch_dot_segsum(c, sc.up(nj), (uint32_t)count, sk, seg_pairs(c, d), cols);
+    return;
+  }
   ntt_list(sc, true, nj, NTT_LOAD_DOT, nullptr, sk->d);
-  if (seg_dev && !out_dev && cols <= SEGSUM_MAX_COLS)
+  if (seg_only)
     HIPCHK(launch_segsum(sc.up(dec), (uint32_t)count, c->d_dc, seg_weights(c, d, cols), c->logn, cols, c->stream));
   else
     HIPCHK(launch_decode(sc.up(dec), (uint32_t)count, c->d_dc, c->d_twist_re, c->d_twist_im, c->d_stage_re,
@@ -1521,6 +1571,15 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->d_fwd_rs = persist(set, fwd);
     set->d_dot_r = persist(set, dot_r);
     set->d_dec_r = persist(set, dec_r);
+    if (nl_r == 1 && segsum_in_transform(c, nb, cols)) {
+      std::vector<NttJob> ds(nb);
+      for (uint32_t bt = 0; bt < nb; ++bt) {
+        const uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
+        ds[bt] = NttJob{r, reinterpret_cast<uint64_t*>(set->sums + (size_t)bt * cols), r + (size_t)Lr * N, nullptr, 0, 0,
+                        scale_r};
+      }
+      set->d_dot_seg = persist(set, ds);
+    }
   }
   set->d_dot_n = persist(set, dot_n);
   set->dot_n_jobs = (uint32_t)dot_n.size();
@@ -1529,6 +1588,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->d_ctpt = persist(set, cp);
   set->d_bjobs = persist(set, bj);
   if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
+  if (set->d_dot_seg) set->seg_p = seg_pairs(c, d);
   HIPCHK(hipStreamSynchronize(c->stream));
 }
 
@@ -1640,13 +1700,15 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       fa.store = NTT_STORE_MUL_RESCALE;
       fa.rc = ctx->d_rc + (size_t)L * L;
       HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
-      launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+      if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
     } else {
       HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
       launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
     }
     const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
-    if (set->seg_w)
+    if (do_rescale && set->d_dot_seg)
+      launch_dot_segsum(ctx, set->d_dot_seg, nb, sk, set->seg_p, set->cols);
+    else if (set->seg_w)
       HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));
     else
       HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,

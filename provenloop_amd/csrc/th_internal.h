@@ -27,7 +27,16 @@ enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_REDUCE =
 // in the evaluation domain: the NTT is linear mod q, so
 //   NTT_q((c_q - (c_last mod q)) * inv) = (C_q - NTT_q(c_last mod q)) * inv
 // for the limb's evaluation-domain input C_q (aux, or the product aux * aux2).
-enum NttStore : uint32_t { NTT_STORE_NONE = 0, NTT_STORE_RESCALE = 1, NTT_STORE_MUL_RESCALE = 2 };
+enum NttStore : uint32_t { NTT_STORE_NONE = 0, NTT_STORE_RESCALE = 1, NTT_STORE_MUL_RESCALE = 2, NTT_STORE_SEGSUM = 3 };
+// NTT_STORE_SEGSUM (inverse, whole-polynomial kernel, limb 0 only): instead of
+// storing the decrypted coefficients m, the transform writes the ZeRo-MOAI
+// segment sums seg[c] = (sum_j v_j W_c[j]) / scale, v_j = m_j centred against
+// q0 / 2 (encoding.rs:221-233), with the segment weights W_c generated from
+// NttArgs::segw (N pairs W_0[j], 2 cos(2 phi_j); segment_weight_pairs) by
+// W_{c+1} = 2 cos(2 phi_j) W_c - W_{c-1}, W_{-1} = W_0; seg = (double*) job
+// dst, scale = job scale.
+constexpr uint32_t NTT_SEGSUM_MAX_COLS = 16;       // standalone segment-sum kernels
+constexpr uint32_t NTT_SEGSUM_FUSED_MAX_COLS = 8;  // NTT_STORE_SEGSUM epilogue (register budget)
 
 // One limb-polynomial transform. In strided mode job i reads src + i*stride,
 // writes dst + i*stride and uses limb limb_base + i % limb_mod.
@@ -38,6 +47,7 @@ struct NttJob {
   const uint64_t* aux2;  // second store operand (MUL_RESCALE)
   uint32_t limb;
   uint32_t pad_;
+  double scale;          // ciphertext scale (SEGSUM)
 };
 
 struct NttArgs {
@@ -53,6 +63,9 @@ struct NttArgs {
   const BarrettConst* bc;     // per limb (MUL, DOT)
   const RescaleConst* rc;     // per limb at the input's level (REDUCE, RESCALE stores)
   const uint64_t* key;        // secret key, L x N (DOT)
+  const double* segw;         // segment weight pairs, N x 2 (SEGSUM)
+  uint32_t cols;              // segments per job (SEGSUM)
+  uint32_t pad_;
 };
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.

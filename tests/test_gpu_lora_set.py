@@ -131,6 +131,22 @@ def test_lora_set_one_column_per_batch(env):
     _check(got, got_sums, exp, exp_sums)
 
 
+@pytest.mark.parametrize("d", [900, 640])
+def test_lora_set_many_columns(env, d):
+    """cols = 9 and 12: more segments than the decrypt transform's fused segment-sum epilogue
+    takes (8), so the standalone segment-sum kernels run; both paths against the oracle."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(d)
+    H = rng.normal(size=(2, d)) * 0.1
+    proj = _projections(rng, 2, d, ranks=[16, 5], d_outs=[32, 7])
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    assert ls.cols == 8192 // d and ls.cols > 8
+    seeds = [41, 42]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, True)
+    _check(got, got_sums, exp, exp_sums)
+
+
 def test_lora_set_device_io_matches_host_io(env):
     eng, ref, sk, pk, rsk, rpk = env
     L = _lib.load()
