@@ -132,7 +132,11 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base) {
   if (!njobs) return hipSuccess;
-  const uint32_t lp = fft_parts_log(logn);
+  // at least one part per LDS budget; more parts (up to 4) while the batch
+  // would leave most CUs idle (the parts are independent workgroups and the
+  // result is the same for any split)
+  uint32_t lp = fft_parts_log(logn);
+  while (lp < 2 && logn - lp > 10 && njobs * (1u << lp) < 256) ++lp;
   const uint32_t M = (1u << logn) >> lp;
   const size_t lds = (size_t)2 * M * sizeof(double);
   const uint32_t gx = (M + 255) / 256 < 32 ? (M + 255) / 256 : 32;

@@ -12,6 +12,8 @@
 // between the two kernels of a split transform (u64 lazy residues, or the
 // bit pattern of the double).
 #pragma once
+#include <type_traits>
+
 #include "th_internal.h"
 
 namespace th {
@@ -116,6 +118,24 @@ struct StoreOp {
   double* seg;
   double scale;
   uint32_t cols;
+  // The stored word for transform output x (the arithmetic's representation)
+  // at position i. Limbs below 2^41 (Fp64Arith) do the rescale in doubles:
+  // exact products without precomputed companions instead of 64-bit Barrett.
+  template <class A>
+  __device__ __forceinline__ uint64_t apply(const A& ar, typename A::V x, uint32_t i) const {
+    if constexpr (std::is_same_v<A, Fp64Arith> && (ST == NTT_STORE_RESCALE || ST == NTT_STORE_MUL_RESCALE)) {
+      const double y = reduce_f64(x, rc.qd, rc.qinv);  // canonical transform output
+      double c;
+      if constexpr (ST == NTT_STORE_MUL_RESCALE)
+        c = mulmod_f64_any(u64_to_f64(gld(aux)[i]), u64_to_f64(gld(aux2)[i]), rc.qd, rc.qinv);
+      else
+        c = u64_to_f64(gld(aux)[i]);
+      const double r = mulmod_f64(c - y, rc.inv_d, rc.inv_dq, rc.qd);  // (c - y) * inv, |c - y| < q
+      return f64_to_u64(r < 0.0 ? r + rc.qd : r);
+    } else {
+      return (*this)(ar.fwd_store(x), i);
+    }
+  }
   __device__ __forceinline__ uint64_t operator()(uint64_t y, uint32_t i) const {
     if constexpr (ST == NTT_STORE_NONE || ST == NTT_STORE_SEGSUM) {
       return y;

@@ -210,7 +210,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
     wave_exchange(x, lds, p2, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so(ar.fwd_store(x[k]), jbase + g(k));
+    for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so.apply(ar, x[k], jbase + g(k));
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
 #pragma unroll

@@ -413,6 +413,10 @@ void build_tables(th_ctx* c) {
       x.inv = invmod(qlast % q, q);
       x.inv_s = (uint64_t)(((u128)x.inv << 64) / q);
       x.b = bc[l];
+      x.qd = (double)q;
+      x.qinv = 1.0 / (double)q;
+      x.inv_d = (double)x.inv;
+      x.inv_dq = (double)x.inv / (double)q;  // correctly rounded: both operands are exact (q < 2^53)
     }
   }
   HIPCHK(hipMalloc(&c->d_rc, rc.size() * sizeof(RescaleConst)));

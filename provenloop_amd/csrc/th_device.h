@@ -152,6 +152,8 @@ __device__ __forceinline__ uint64_t submod(uint64_t a, uint64_t b, uint64_t q) {
 struct RescaleConst {
   uint64_t q, inv, inv_s;  // q_l, (q_last mod q_l)^{-1} and its Shoup companion
   BarrettConst b;          // remainder of a 64-bit value modulo q_l
+  double qd, qinv;         // q_l and 1/q_l as doubles (limbs below 2^41)
+  double inv_d, inv_dq;    // inv and inv / q_l as doubles (limbs below 2^41)
 };
 
 // ---------------------------------------------------------------- fp64 path
@@ -162,6 +164,19 @@ __device__ __forceinline__ double mulmod_f64(double x, double w, double wq, doub
   double quot = __builtin_rint(x * wq);
   double r = __fma_rn(-quot, q, hi);
   return r + lo;
+}
+
+// a*b mod q in [0, q) for integers 0 <= a, b < q < 2^41 held exactly in
+// doubles, without a precomputed companion: hi + lo = a*b exactly (one FMA),
+// and quot = rint(hi / q) through qinv = 1/q is within 0.5 + 2^-10 of a*b/q
+// (a*b/q < 2^41, relative error below 2^-51), so r = a*b - quot*q, formed
+// exactly, lies in (-q, q).
+__device__ __forceinline__ double mulmod_f64_any(double a, double b, double q, double qinv) {
+  const double hi = a * b;
+  const double lo = __fma_rn(a, b, -hi);
+  const double quot = __builtin_rint(hi * qinv);
+  const double r = __fma_rn(-quot, q, hi) + lo;
+  return r < 0.0 ? r + q : r;
 }
 
 // x mod q into [0, q) for an exact integer |x| < 2^50.
