@@ -118,35 +118,62 @@ struct StoreOp {
   double* seg;
   double scale;
   uint32_t cols;
-  // The stored word for transform output x (the arithmetic's representation)
-  // at position i. Limbs below 2^41 (Fp64Arith) do the rescale in doubles:
-  // exact products without precomputed companions instead of 64-bit Barrett.
+  // Operands the store reads at position i (ct x pt factors, or the value the
+  // rescale subtracts from); loaded apart from the arithmetic so that a pass
+  // can issue these loads early and hide their latency behind its butterflies.
+  static constexpr int NAUX = ST == NTT_STORE_MUL_RESCALE ? 2 : ST == NTT_STORE_RESCALE ? 1 : 0;
+  struct Aux {
+    uint64_t a, b;
+  };
+  __device__ __forceinline__ Aux load_aux(uint32_t i) const {
+    Aux v{0, 0};
+    if constexpr (NAUX >= 1) v.a = gld(aux)[i];
+    if constexpr (NAUX >= 2) v.b = gld(aux2)[i];
+    return v;
+  }
+  // The value the rescale subtracts from (ct x pt product, or the single
+  // operand), reduced modulo q, from the operands v: a double's bit pattern
+  // on limbs below 2^41 (Fp64Arith), else the residue.
   template <class A>
-  __device__ __forceinline__ uint64_t apply(const A& ar, typename A::V x, uint32_t i) const {
-    if constexpr (std::is_same_v<A, Fp64Arith> && (ST == NTT_STORE_RESCALE || ST == NTT_STORE_MUL_RESCALE)) {
-      const double y = reduce_f64(x, rc.qd, rc.qinv);  // canonical transform output
+  __device__ __forceinline__ uint64_t prep(const A&, const Aux& v) const {
+    if constexpr (NAUX == 0) {
+      return 0;
+    } else if constexpr (std::is_same_v<A, Fp64Arith>) {
       double c;
       if constexpr (ST == NTT_STORE_MUL_RESCALE)
-        c = mulmod_f64_any(u64_to_f64(gld(aux)[i]), u64_to_f64(gld(aux2)[i]), rc.qd, rc.qinv);
+        c = mulmod_f64_any(u64_to_f64(v.a), u64_to_f64(v.b), rc.qd, rc.qinv);
       else
-        c = u64_to_f64(gld(aux)[i]);
+        c = u64_to_f64(v.a);
+      return __builtin_bit_cast(uint64_t, c);
+    } else {
+      if constexpr (ST == NTT_STORE_MUL_RESCALE)
+        return mulmod_barrett(v.a, v.b, bc);
+      else
+        return v.a;
+    }
+  }
+  // The stored word for transform output x (the arithmetic's representation)
+  // with the prepared value c of its position (prep). Limbs below 2^41
+  // (Fp64Arith) do the rescale in doubles: exact products without
+  // precomputed companions instead of 64-bit Barrett.
+  template <class A>
+  __device__ __forceinline__ uint64_t apply_prep(const A& ar, typename A::V x, uint64_t cp) const {
+    if constexpr (std::is_same_v<A, Fp64Arith> && NAUX > 0) {
+      const double y = reduce_f64(x, rc.qd, rc.qinv);  // canonical transform output
+      const double c = __builtin_bit_cast(double, cp);
       const double r = mulmod_f64(c - y, rc.inv_d, rc.inv_dq, rc.qd);  // (c - y) * inv, |c - y| < q
       return f64_to_u64(r < 0.0 ? r + rc.qd : r);
     } else {
-      return (*this)(ar.fwd_store(x), i);
+      const uint64_t y = ar.fwd_store(x);
+      if constexpr (NAUX == 0)
+        return y;
+      else
+        return csub(shoup_lazy(submod(cp, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
     }
   }
-  __device__ __forceinline__ uint64_t operator()(uint64_t y, uint32_t i) const {
-    if constexpr (ST == NTT_STORE_NONE || ST == NTT_STORE_SEGSUM) {
-      return y;
-    } else {
-      uint64_t c;
-      if constexpr (ST == NTT_STORE_MUL_RESCALE)
-        c = mulmod_barrett(gld(aux)[i], gld(aux2)[i], bc);
-      else
-        c = gld(aux)[i];
-      return csub(shoup_lazy(submod(c, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
-    }
+  template <class A>
+  __device__ __forceinline__ uint64_t apply(const A& ar, typename A::V x, uint32_t i) const {
+    return apply_prep(ar, x, prep(ar, load_aux(i)));
   }
 };
 
