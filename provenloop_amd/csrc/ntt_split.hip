@@ -324,21 +324,26 @@ __global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs
 #pragma unroll
     for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
   }
+  // c mod q_l: FP64 on limbs below 2^41, else Barrett when c >= q_l
   for (uint32_t f = 0; f < nf; ++f) {
     const NttJob fj = fwd.jobs[(uint64_t)job * nf + f];
     const LimbConst& lcf = fwd.lc[fj.limb];
     const RescaleConst rc = fwd.rc[fj.limb];
+    // c is the same at every iteration; hiding that keeps the compiler from
+    // hoisting per-coefficient terms out of the loop into extra registers
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = opaque_u64(c[k]);
     if (lcf.fp64) {
       const Fp64Arith ar(lcf);
       Fp64Arith::V x[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b));
+      for (int k = 0; k < 16; ++k) x[k] = reduce_u64_f64(c[k], rc);
       column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
     } else {
       const IntArith ar(lcf);
       IntArith::V x[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b));
+      for (int k = 0; k < 16; ++k) x[k] = c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b);
       column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
     }
   }

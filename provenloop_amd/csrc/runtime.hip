@@ -417,6 +417,8 @@ void build_tables(th_ctx* c) {
       x.qinv = 1.0 / (double)q;
       x.inv_d = (double)x.inv;
       x.inv_dq = (double)x.inv / (double)q;  // correctly rounded: both operands are exact (q < 2^53)
+      x.k32 = (double)((1ULL << 32) % q);
+      x.k32q = x.k32 / (double)q;
     }
   }
   HIPCHK(hipMalloc(&c->d_rc, rc.size() * sizeof(RescaleConst)));

@@ -154,6 +154,7 @@ struct RescaleConst {
   BarrettConst b;          // remainder of a 64-bit value modulo q_l
   double qd, qinv;         // q_l and 1/q_l as doubles (limbs below 2^41)
   double inv_d, inv_dq;    // inv and inv / q_l as doubles (limbs below 2^41)
+  double k32, k32q;        // 2^32 mod q_l and that / q_l as doubles (limbs below 2^41)
 };
 
 // ---------------------------------------------------------------- fp64 path
@@ -164,6 +165,16 @@ __device__ __forceinline__ double mulmod_f64(double x, double w, double wq, doub
   double quot = __builtin_rint(x * wq);
   double r = __fma_rn(-quot, q, hi);
   return r + lo;
+}
+
+// c mod q_l for any c < 2^61 on a limb below 2^41, as an exact double in
+// [0, q_l): with c = ch 2^32 + cl (ch < 2^29), c = ch (2^32 mod q_l) + cl
+// (mod q_l), the first term an exact FP64 product in (-q_l, q_l) and cl < q_l.
+__device__ __forceinline__ double reduce_u64_f64(uint64_t c, const RescaleConst& rc) {
+  const double ch = (double)(uint32_t)(c >> 32), cl = (double)(uint32_t)c;
+  double r = mulmod_f64(ch, rc.k32, rc.k32q, rc.qd) + cl;  // (-q_l, 2 q_l)
+  r = r < 0.0 ? r + rc.qd : r;
+  return r >= rc.qd ? r - rc.qd : r;
 }
 
 // a*b mod q in [0, q) for integers 0 <= a, b < q < 2^41 held exactly in
