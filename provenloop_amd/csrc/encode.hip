@@ -27,28 +27,63 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   const uint32_t part = blockIdx.x;
   const EncodeJob jb = jobs[blockIdx.y];
   const GPtr<double> z = gld(z_base ? z_base + (size_t)blockIdx.y * (jb.rep_d ? jb.rep_d : S) : jb.z);
+  const uint32_t MP = fft_pad(M);  // padded length of re and im
   double* re = sh;
-  double* im = sh + M;
+  double* im = sh + MP;
   const uint32_t r = brv_bits(part, LP);
   const uint32_t lb = logn - LP;
-  for (uint32_t jj = threadIdx.x; jj < M; jj += blockDim.x) {
-    const uint32_t j = (jj << LP) | r;  // element at bit-reversed position part*M + pos
-    const uint32_t pos = brv_bits(jj, lb);
-    const uint32_t slot = j < S ? j : n - 1 - j;
-    double v;
-    if (jb.rep_d)  // inference_engine.py:1266-1269: [h | h | ... | 0]
-      v = slot < jb.rep_cols * jb.rep_d ? z[slot % jb.rep_d] : 0.0;
-    else
-      v = z[slot];
-    re[pos] = v;
-    im[pos] = 0.0;
+  // With 8 or more parts the in-part stages' twiddles (entries 0 .. M-2 of
+  // the stage tables) are staged in LDS beside the values, read in the same
+  // coalesced phase as the input instead of once per register pass.
+  constexpr bool TWL = LP >= 3;
+  const double* twr = stage_re;
+  const double* twi = stage_im;
+  if constexpr (TWL) {
+    double* tr = sh + 2 * MP;
+    double* ti = sh + 2 * MP + M;
+    for (uint32_t i = threadIdx.x; i + 1 < M; i += blockDim.x) {
+      tr[i] = gld(stage_re)[i];
+      ti[i] = gld(stage_im)[i];
+    }
+    twr = tr;
+    twi = ti;
+  }
+  // input gather, 8 values per thread per round: all loads issued before the
+  // first LDS store
+  constexpr int FV = 8;
+  for (uint32_t j0 = threadIdx.x; j0 < M; j0 += FV * blockDim.x) {
+    double v[FV];
+#pragma unroll
+    for (int e = 0; e < FV; ++e) {
+      const uint32_t jj = j0 + e * blockDim.x;
+      const bool in = jj < M;
+      const uint32_t j = ((in ? jj : 0) << LP) | r;  // element at bit-reversed position part*M + brv(jj)
+      const uint32_t slot = j < S ? j : n - 1 - j;
+      bool keep = in;
+      uint32_t idx = slot;
+      if (jb.rep_d) {  // inference_engine.py:1266-1269: [h | h | ... | 0]
+        keep = keep && slot < jb.rep_cols * jb.rep_d;
+        idx = keep ? slot % jb.rep_d : 0;
+      }
+      const double t = z[idx];  // unconditional (index 0 when unused), so the loads issue together
+      v[e] = keep ? t : 0.0;
+    }
+#pragma unroll
+    for (int e = 0; e < FV; ++e) {
+      const uint32_t jj = j0 + e * blockDim.x;
+      if (jj < M) {
+        const uint32_t pos = fft_pad(brv_bits(jj, lb));
+        re[pos] = v[e];
+        im[pos] = 0.0;
+      }
+    }
   }
   __syncthreads();
-  dit_stages_reg(re, im, lb, stage_re, stage_im);
+  dit_stages_reg<true>(re, im, lb, twr, twi);
   const GMut<double> out = gst(jb.parts) + (size_t)part * 2 * M;
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
-    out[i] = re[i];
-    out[M + i] = im[i];
+    out[i] = re[fft_pad(i)];
+    out[M + i] = im[fft_pad(i)];
   }
 }
 
@@ -61,12 +96,6 @@ __device__ __forceinline__ int64_t round_sat_i64(double x) {
   return (int64_t)r;
 }
 
-__device__ __forceinline__ uint64_t signed_residue_dev(int64_t e, const BarrettConst& m) {
-  const uint64_t a = e >= 0 ? (uint64_t)e : (uint64_t)0 - (uint64_t)e;
-  const uint64_t r = a < m.q ? a : mulmod_barrett(a, 1, m);
-  return e >= 0 ? r : m.q - r;
-}
-
 __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const BarrettConst* __restrict__ bc,
                                                  const double* __restrict__ twist_re,
                                                  const double* __restrict__ twist_im, uint32_t j, Cx a,
@@ -75,6 +104,10 @@ __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const Barr
   const double a_im = a.im * inv_n;
   const double coeff = a_re * twist_re[j] + a_im * twist_im[j];
   const int64_t m = round_sat_i64(coeff * 1099511627776.0);  // * 2^40 (params.rs:12)
+  if (jb.mvals) {
+    gst(jb.mvals)[j] = m;
+    return;
+  }
   const int64_t e0 = jb.e0 ? gld(jb.e0)[j] : 0;
   const int64_t e1 = jb.e1 ? gld(jb.e1)[j] : 0;
   const uint8_t u = jb.u ? gld(jb.u)[j] : 1;  // ciphertext.rs:261-266: 0 -> q-1, 1 -> 0, 2 -> 1
@@ -88,6 +121,13 @@ __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const Barr
   }
 }
 
+// The last LP stages combine element k of every part: position p*M + k of
+// stage lb + t pairs with the part whose index differs in bit t, and its
+// twiddle index is its position modulo the stage's half size, (p mod 2^t)*M + k,
+// the same operands and twiddles as dit_stages_lds, so the result is
+// bit-identical to one transform of N values. G = 2^LP / 4 threads share a
+// position k (thread o of them emits parts s*G + o); each recomputes the
+// small combine, which costs far less than the residues it writes.
 template <int LP>
 __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restrict__ jobs,
                                                       const BarrettConst* __restrict__ bc,
@@ -96,32 +136,36 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
                                                       const double* __restrict__ stage_re,
                                                       const double* __restrict__ stage_im, uint32_t logn,
                                                       uint32_t L) {
-  const uint32_t n = 1u << logn;
+  constexpr int P = 1 << LP;
+  constexpr int G = P >= 4 ? P / 4 : 1;
+  const uint32_t n = 1u << logn, lb = logn - LP;
   const uint32_t M = n >> LP;
   const EncodeJob jb = jobs[blockIdx.y];
-  const GPtr<double> P = gld(jb.parts);
+  const GPtr<double> Pd = gld(jb.parts);
+  const GPtr<double> wr = gld(stage_re), wi = gld(stage_im);
   const double inv_n = 1.0 / (double)n;
-  auto at = [&](uint32_t part, uint32_t i) { return Cx{P[(size_t)part * 2 * M + i], P[(size_t)part * 2 * M + M + i]}; };
-  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < M; k += gridDim.x * blockDim.x) {
-    if constexpr (LP == 0) {
-      emit_coefficient(jb, bc, twist_re, twist_im, k, at(0, k), inv_n, n, L);
-    } else if constexpr (LP == 1) {
-      const uint32_t S = n / 2;
-      Cx t, b;
-      dit(at(0, k), at(1, k), stage_re[S - 1 + k], stage_im[S - 1 + k], t, b);
-      emit_coefficient(jb, bc, twist_re, twist_im, k, t, inv_n, n, L);
-      emit_coefficient(jb, bc, twist_re, twist_im, k + S, b, inv_n, n, L);
-    } else {  // LP == 2
-      const uint32_t S = n / 2, Q4 = n / 4;
-      Cx y0, y1, y2, y3, o0, o1, o2, o3;
-      dit(at(0, k), at(1, k), stage_re[Q4 - 1 + k], stage_im[Q4 - 1 + k], y0, y1);
-      dit(at(2, k), at(3, k), stage_re[Q4 - 1 + k], stage_im[Q4 - 1 + k], y2, y3);
-      dit(y0, y2, stage_re[S - 1 + k], stage_im[S - 1 + k], o0, o2);
-      dit(y1, y3, stage_re[S - 1 + k + Q4], stage_im[S - 1 + k + Q4], o1, o3);
-      emit_coefficient(jb, bc, twist_re, twist_im, k, o0, inv_n, n, L);
-      emit_coefficient(jb, bc, twist_re, twist_im, k + Q4, o1, inv_n, n, L);
-      emit_coefficient(jb, bc, twist_re, twist_im, k + S, o2, inv_n, n, L);
-      emit_coefficient(jb, bc, twist_re, twist_im, k + S + Q4, o3, inv_n, n, L);
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < G * M; i += gridDim.x * blockDim.x) {
+    const uint32_t o = i >> lb, k = i & (M - 1);  // o is uniform over a wavefront (M >= 64)
+    Cx x[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) x[p] = Cx{Pd[(size_t)p * 2 * M + k], Pd[(size_t)p * 2 * M + M + k]};
+#pragma unroll
+    for (int t = 0; t < LP; ++t) {
+      const uint32_t half = M << t;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        if (p & (1 << t)) continue;
+        const uint32_t w = half - 1 + (uint32_t)(p & ((1 << t) - 1)) * M + k;
+        dit(x[p], x[p | (1 << t)], wr[w], wi[w], x[p], x[p | (1 << t)]);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < P / G; ++s) {
+      Cx v = x[s * G];
+#pragma unroll
+      for (int g = 1; g < G; ++g)
+        if (o == (uint32_t)g) v = x[s * G + g];
+      emit_coefficient(jb, bc, twist_re, twist_im, (uint32_t)(s * G) * M + o * M + k, v, inv_n, n, L);
     }
   }
 }
@@ -132,22 +176,26 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base) {
   if (!njobs) return hipSuccess;
-  // at least one part per LDS budget; more parts (up to 4) while the batch
-  // would leave most CUs idle (the parts are independent workgroups and the
-  // result is the same for any split)
+  // at least one part per LDS budget; more parts (up to 16, of at least 1024
+  // values) while the batch would leave CUs idle: the parts are independent
+  // workgroups and the result is the same for any split
   uint32_t lp = fft_parts_log(logn);
-  while (lp < 2 && logn - lp > 10 && njobs * (1u << lp) < 256) ++lp;
+  while (lp < 4 && logn - lp > 10 && njobs * (1u << lp) < 512) ++lp;
   const uint32_t M = (1u << logn) >> lp;
-  const size_t lds = (size_t)2 * M * sizeof(double);
-  const uint32_t gx = (M + 255) / 256 < 32 ? (M + 255) / 256 : 32;
+  // padded values (+ twiddles with 8 or more parts)
+  const size_t lds = ((size_t)2 * fft_pad(M) + (lp >= 3 ? (size_t)2 * M : 0)) * sizeof(double);
+  // dit_stages_reg needs 8 values per thread at most
+  const uint32_t threads = M / 8 < 64 ? 64 : (M / 8 > ENC_THREADS ? ENC_THREADS : M / 8);
+  const uint32_t fin = lp >= 2 ? M << (lp - 2) : M;  // threads of the final kernel per encode
+  const uint32_t gx = (fin + 255) / 256 < 32 ? (fin + 255) / 256 : 32;
   hipError_t e;
 #define TH_ENC(LP)                                                                                         \
   case LP:                                                                                                 \
     e = hipFuncSetAttribute((const void*)k_encode_parts<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
                             (int)lds);                                                                     \
     if (e != hipSuccess) return e;                                                                         \
-    hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(ENC_THREADS), lds, s, jobs,         \
-                       stage_re, stage_im, logn, z_base);                                                  \
+    hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
+                       stage_im, logn, z_base);                                                            \
     hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im, \
                        stage_re, stage_im, logn, L);                                                       \
     return hipGetLastError();
@@ -155,6 +203,8 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
     TH_ENC(0)
     TH_ENC(1)
     TH_ENC(2)
+    TH_ENC(3)
+    TH_ENC(4)
     default: return hipErrorInvalidValue;
   }
 #undef TH_ENC

@@ -12,6 +12,8 @@ struct EncodeJob {
   const int64_t* e0;   // rounded Gaussian e0, or null (plain encode)
   const int64_t* e1;   // rounded Gaussian e1, or null
   uint64_t* dst;       // [M (L) | E1 (L) | U (L)] limb-polys; only M when e1/u are null
+  int64_t* mvals;      // non-null: write m itself (N i64) instead of dst (the residues are then
+                       // formed by the encrypt transforms' loads, NTT_LOAD_ENC)
   double* parts;       // scratch, encode_parts_doubles(logn) doubles
 };
 

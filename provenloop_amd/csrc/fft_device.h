@@ -62,10 +62,17 @@ __device__ __forceinline__ void dit_stages_lds(double* re, double* im, uint32_t 
 // differ only in those bits, runs the R stages on them and writes them back,
 // so LDS is read and written once per pass instead of once per stage. Every
 // butterfly sees the same operands and twiddle as in dit_stages_lds, so the
-// result is bit-identical. Needs blockDim.x * 8 >= M.
+// result is bit-identical. Needs blockDim.x * 8 >= M. With PAD, value i
+// lives at re/im[i + i / 8] (fft_pad): one spare slot per 8 values puts the
+// lanes of the first two passes (8 consecutive values per lane, and groups of
+// 8 lanes 64 values apart) on different LDS banks.
+__host__ __device__ constexpr uint32_t fft_pad(uint32_t i) { return i + (i >> 3); }
+
+template <bool PAD = false>
 __device__ __forceinline__ void dit_stages_reg(double* re, double* im, uint32_t lb,
                                                const double* __restrict__ stage_re,
                                                const double* __restrict__ stage_im) {
+  auto P = [](uint32_t i) { return PAD ? fft_pad(i) : i; };
   const uint32_t M = 1u << lb;
   for (uint32_t s0 = 0; s0 < lb; s0 += 3) {
     const uint32_t R = lb - s0 < 3 ? lb - s0 : 3;
@@ -76,7 +83,7 @@ __device__ __forceinline__ void dit_stages_reg(double* re, double* im, uint32_t 
       Cx x[8];
 #pragma unroll
       for (uint32_t r = 0; r < 8; ++r)
-        if (r < (1u << R)) x[r] = Cx{re[base | (r << s0)], im[base | (r << s0)]};
+        if (r < (1u << R)) x[r] = Cx{re[P(base | (r << s0))], im[P(base | (r << s0))]};
 #pragma unroll
       for (uint32_t rb = 0; rb < 3; ++rb) {
         if (rb >= R) break;
@@ -95,8 +102,8 @@ __device__ __forceinline__ void dit_stages_reg(double* re, double* im, uint32_t 
 #pragma unroll
       for (uint32_t r = 0; r < 8; ++r)
         if (r < (1u << R)) {
-          re[base | (r << s0)] = x[r].re;
-          im[base | (r << s0)] = x[r].im;
+          re[P(base | (r << s0))] = x[r].re;
+          im[P(base | (r << s0))] = x[r].im;
         }
     }
     __syncthreads();

@@ -96,7 +96,35 @@ struct LoadOp {
   const uint64_t* key;  // secret-key limb-poly (DOT)
   BarrettConst bc;
   RescaleConst rc;
+  uint32_t sub;         // ENC variant (uniform over the job)
+  double qd, qinv;      // q and 1/q as doubles (ENC)
+  // signed_residue_dev with |e| in [q, 2^53) reduced by one exact FP64 step:
+  // quot = rint(|e| / q) is within one of the true quotient, and the remainder
+  // fma(-quot, q, |e|) is an exact integer in (-q, q)
+  __device__ __forceinline__ uint64_t enc_residue(int64_t e) const {
+    const uint64_t a = e >= 0 ? (uint64_t)e : (uint64_t)0 - (uint64_t)e;
+    uint64_t r = a;
+    if (a >= bc.q) {
+      if (a < (1ULL << 53)) {
+        const double ad = u64_to_f64(a);
+        double t = __fma_rn(-__builtin_rint(ad * qinv), qd, ad);
+        t = t < 0.0 ? t + qd : t;
+        r = f64_to_u64(t >= qd ? t - qd : t);
+      } else {
+        r = mulmod_barrett(a, 1, bc);
+      }
+    }
+    return e >= 0 ? r : bc.q - r;
+  }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
+    if constexpr (LD == NTT_LOAD_ENC) {
+      if (sub == 2) {
+        const uint8_t u = gld(reinterpret_cast<const uint8_t*>(src))[i];
+        return u == 0 ? bc.q - 1 : (u == 1 ? 0 : 1);
+      }
+      const uint64_t r = enc_residue((int64_t)gld(src)[i]);
+      return sub == 0 ? csub(r + enc_residue((int64_t)gld(aux)[i]), bc.q) : r;
+    }
     const uint64_t x = gld(src)[i];
     if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
     if constexpr (LD == NTT_LOAD_REDUCE) return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
@@ -182,7 +210,12 @@ template <uint32_t LD, uint32_t ST>
 __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint32_t limb, uint32_t n,
                                         LoadOp<LD>& op, StoreOp<ST>& so) {
   op.aux = jb.aux;
-  if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT) op.bc = a.bc[limb];
+  if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT || LD == NTT_LOAD_ENC) op.bc = a.bc[limb];
+  if constexpr (LD == NTT_LOAD_ENC) {
+    op.sub = jb.sub;
+    op.qd = a.lc[limb].qd;
+    op.qinv = a.lc[limb].qinv;
+  }
   if constexpr (LD == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * n;
   if constexpr (LD == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
   so.aux = jb.aux;
@@ -198,13 +231,14 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 }
 
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
-// Only the pairs the engine issues are instantiated: forward (NONE, NONE),
-// (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT, NONE),
-// (DOT, SEGSUM).
+// Only the pairs the engine issues are instantiated: forward (NONE | ENC,
+// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT,
+// NONE), (DOT, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   if constexpr (!INV) {
     if (load == NTT_LOAD_NONE && store == NTT_STORE_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_ENC && store == NTT_STORE_NONE) return f.template operator()<NTT_LOAD_ENC, NTT_STORE_NONE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_RESCALE)
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_RESCALE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_MUL_RESCALE)

@@ -208,6 +208,7 @@ struct th_lora {
   double* hidden = nullptr;    // n_in x d
   uint8_t* u = nullptr;        // n_in x N
   int64_t *e0 = nullptr, *e1 = nullptr;
+  int64_t* mvals = nullptr;    // n_in x N encoded messages m (i64)
   uint64_t* prep = nullptr;    // n_in x 3L x N
   uint64_t* cts = nullptr;     // n_in x 2L x N
   uint64_t* work = nullptr;    // n_batches x 2L x N: rescale inverse transforms, or the products
@@ -219,6 +220,7 @@ struct th_lora {
   const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
   const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr, *d_dot_n = nullptr;
+  const NttJob* d_enc_ntt = nullptr;  // encrypt transforms: residues of m + e0, e1, u formed in the loads
   const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
   const CtPtJob* d_ctpt = nullptr;
@@ -1492,6 +1494,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->u = (uint8_t*)set->alloc((size_t)ni * N);
   set->e0 = (int64_t*)set->alloc((size_t)ni * N * 8);
   set->e1 = (int64_t*)set->alloc((size_t)ni * N * 8);
+  set->mvals = (int64_t*)set->alloc((size_t)ni * N * 8);
   set->prep = (uint64_t*)set->alloc(ni * 3 * L * P);
   double* enc_parts = (double*)set->alloc(ni * encode_parts_doubles(c->logn) * 8);
   set->cts = (uint64_t*)set->alloc(ni * 2 * L * P);
@@ -1534,9 +1537,26 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     ej[i].e0 = set->e0 + (size_t)i * N;
     ej[i].e1 = set->e1 + (size_t)i * N;
     ej[i].dst = set->prep + (size_t)i * 3 * L * N;
+    ej[i].mvals = set->mvals + (size_t)i * N;
     ej[i].parts = enc_parts + i * encode_parts_doubles(c->logn);
   }
   set->d_enc = persist(set, ej);
+  {
+    // the encrypt inputs' forward transforms read m, e0, e1 and u and form
+    // each limb's residues as they load them: [M_l = m + e0 | E1_l | U_l] per input
+    std::vector<NttJob> ej2;
+    for (uint32_t i = 0; i < ni; ++i) {
+      uint64_t* pr = set->prep + (size_t)i * 3 * L * N;
+      const uint64_t* m = reinterpret_cast<const uint64_t*>(set->mvals + (size_t)i * N);
+      const uint64_t* e0 = reinterpret_cast<const uint64_t*>(set->e0 + (size_t)i * N);
+      const uint64_t* e1 = reinterpret_cast<const uint64_t*>(set->e1 + (size_t)i * N);
+      const uint64_t* u = reinterpret_cast<const uint64_t*>(set->u + (size_t)i * N);
+      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{m, pr + (size_t)l * N, e0, nullptr, l, 0});
+      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{e1, pr + (size_t)(L + l) * N, nullptr, nullptr, l, 1});
+      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{u, pr + (size_t)(2 * L + l) * N, nullptr, nullptr, l, 2});
+    }
+    set->d_enc_ntt = persist(set, ej2);
+  }
   std::vector<NttJob> inv, fwd, dot_r, dot_n;
   std::vector<DecodeJob> dec_r(nb), dec_n(nb);
   std::vector<CtPtJob> cp(nb);
@@ -1692,7 +1712,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true));
     HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
                          ctx->d_stage_im, ctx->logn, L, st, z));
-    ntt_strided(ctx, false, set->prep, set->prep, ni * 3 * L, L);
+    launch_jobs_ntt(ctx, false, set->d_enc_ntt, ni * 3 * L, NTT_LOAD_ENC);
     HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
     if (do_rescale) {
       // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones

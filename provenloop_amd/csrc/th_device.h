@@ -144,6 +144,13 @@ __device__ __forceinline__ uint64_t mulmod_barrett(uint64_t a, uint64_t b, const
 
 __device__ __forceinline__ uint64_t addmod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
 
+// e >= 0 ? e mod q : q - (|e| mod q) (ciphertext.rs:132-136, :275-287; encoding.rs:198-202)
+__device__ __forceinline__ uint64_t signed_residue_dev(int64_t e, const BarrettConst& m) {
+  const uint64_t a = e >= 0 ? (uint64_t)e : (uint64_t)0 - (uint64_t)e;
+  const uint64_t r = a < m.q ? a : mulmod_barrett(a, 1, m);
+  return e >= 0 ? r : m.q - r;
+}
+
 __device__ __forceinline__ uint64_t submod(uint64_t a, uint64_t b, uint64_t q) {
   return a >= b ? a - b : a + q - b;
 }

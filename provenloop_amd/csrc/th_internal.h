@@ -16,7 +16,11 @@ namespace th {
 //                                                         taken to limb q: rescale)
 //   DOT      x = src[i] + aux[i] * key[i] mod q, src = c0, aux = c1, key = s
 //                                                         (decrypt, ciphertext.rs:332-341)
-enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_REDUCE = 2, NTT_LOAD_DOT = 3 };
+//   ENC      the encrypt_pk inputs' residues (ciphertext.rs:256-296), by the job's sub:
+//            0: x = (m + e0) mod q, src = m, aux = e0 (i64 coefficients)
+//            1: x = e1 mod q, src = e1 (i64)
+//            2: x = u mapped 0 -> q-1, 1 -> 0, 2 -> 1, src = u (u8)
+enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_REDUCE = 2, NTT_LOAD_DOT = 3, NTT_LOAD_ENC = 4 };
 
 // Operation applied to every output of a FORWARD transform before it is
 // stored (fused consumer), y = the transformed value in [0, q):
@@ -46,7 +50,7 @@ struct NttJob {
   const uint64_t* aux;   // operand of the load or store operation
   const uint64_t* aux2;  // second store operand (MUL_RESCALE)
   uint32_t limb;
-  uint32_t pad_;
+  uint32_t sub;          // variant of the load operation (ENC)
   double scale;          // ciphertext scale (SEGSUM)
 };
 
