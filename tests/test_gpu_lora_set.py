@@ -85,6 +85,27 @@ def test_lora_set_matches_oracle(env, rescale):
     assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=rescale), got_sums)
 
 
+@pytest.mark.parametrize("scale", [3e3, 1e7, 1e12])
+def test_lora_set_large_inputs(env, scale):
+    """Hidden states whose encoded coefficients |m| exceed the 40-bit primes (3e3: about 2^45, the
+    FP64 residue step), straddle 2^53 (1e7: FP64 step and 64-bit Barrett fallback), or saturate the
+    encoder's rounding (1e12): the encrypt transforms' fused residues (m + e0, e1, u formed in the
+    loads) equal the encoder-written residues of th_lora_a_pass bit for bit, and the segment sums
+    match the oracle's."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(int(scale) % 1000)
+    H = rng.normal(size=(1, 1536)) * scale
+    proj = [(0, rng.normal(size=(5, 1536)) * 0.02, rng.normal(size=(8, 5)) * 0.02)]
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    seeds = [777]
+    for rescale in (True, False):
+        got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=rescale, with_intermediates=True)
+        pts = [eng.encode_to_ntt(p) for p in zero_moai.pack_rows(proj[0][1], 8192)]
+        assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, [0], rescale=rescale), got_sums)
+        exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, rescale)
+        assert np.max(np.abs(got_sums - exp_sums)) <= 1e-9 * max(1.0, np.max(np.abs(exp_sums)))
+
+
 def test_lora_set_full_token_shape(env):
     """28 layers x {q, v} (224 products: the launches take the split-NTT path); layers 0 and 27
     against the oracle, and the device-resident run equal to the host-I/O run."""
