@@ -102,14 +102,21 @@ __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, G
 // Re-distribute the wavefront's 16 x 64 coefficients from layout `from` to
 // layout `to` (functions of the register index giving the index e in
 // [0, 1024)) through its LDS slice.
+// The slice is the wavefront's own, so a wavefront-level barrier orders it.
+__device__ __forceinline__ void slice_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <class V, class From, class To>
 __device__ __forceinline__ void wave_exchange(V (&x)[16], V* lds, From from, To to) {
 #pragma unroll
   for (int k = 0; k < 16; ++k) lds[pad16(from(k))] = x[k];
-  __syncthreads();
+  slice_sync();
 #pragma unroll
   for (int k = 0; k < 16; ++k) x[k] = lds[pad16(to(k))];
-  __syncthreads();
+  slice_sync();
 }
 
 // ------------------------------------------------------------------ column pass
@@ -185,6 +192,31 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
 }
 
 // ------------------------------------------------------------------ row pass
+// Forward row pass of part `part` from the column pass's intermediate in buf;
+// leaves the transform's outputs (the arithmetic's representation) in
+// registers in the lane-contiguous layout G: x[k] is element part * 1024 +
+// lane + 64 k.
+template <int LOGN, class A>
+__device__ __forceinline__ void row_fwd_regs(typename A::V (&x)[16], const uint64_t* buf, const LimbConst& lc,
+                                             const A& ar, uint32_t part, uint64_t* lds_raw) {
+  constexpr int CB = Split<LOGN>::CB, M = (1 << (CB - 4)) - 1;
+  const uint32_t l = threadIdx.x & 63;
+  const uint32_t jbase = part << 10;
+  const uint32_t rowbits = (l >> (CB - 4)) << CB;
+  auto p1 = [&](uint32_t k) { return (l & M) | (k << (CB - 4)) | rowbits; };
+  auto p2 = [&](uint32_t k) { return k | ((l & M) << 4) | rowbits; };
+  auto g = [&](uint32_t k) { return l + 64 * k; };
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  const GPtr<uint64_t> gbuf = gld(buf);
+  const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gbuf[jbase + p1(k)]);
+  fwd_stages<LOGN, CB - 4, CB - 1, CB - 4>(x, jbase + p1(0), tw, ar);
+  wave_exchange(x, lds, p1, p2);
+  fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
+  wave_exchange(x, lds, p2, g);
+}
+
 template <int LOGN, bool INV, class A, class LOp, class SOp>
 __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
                                          const LimbConst& lc, const LOp& op, const SOp& so, uint32_t part,
@@ -376,6 +408,79 @@ hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, con
     case 13: return launch_rescale_t<13>(inv, ninv, fwd, nf, s);
     case 14: return launch_rescale_t<14>(inv, ninv, fwd, nf, s);
     case 15: return launch_rescale_t<15>(inv, ninv, fwd, nf, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Encrypt row kernel: the forward row passes of one input's M_l, U_l and E1_l
+// (their column passes, with the residues formed in the loads, have left the
+// intermediates in the jobs' dst), combined as they are stored into
+//   c0_l = b_l * U_l + M_l,  c1_l = a_l * U_l + E1_l   (ciphertext.rs:298-312)
+// so the three transforms are never written out. Workgroup w works on part
+// w % PARTS of input / limb w / PARTS with three wavefronts, one per
+// transform (0: M, 1: U, 2: E1), each with its own LDS slice; U's wavefront
+// hands its canonical outputs to the other two through LDS, which form and
+// store c0 and c1. jobs: 3L per input (M_0..M_{L-1}, E1_0.., U_0..);
+// pk = [b (L) | a (L)]; input i's ciphertext at cts + i 2 L N.
+template <int LOGN>
+__global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pk, uint64_t* cts, uint32_t L) {
+  using S = Split<LOGN>;
+  __shared__ uint64_t lds[3][S::LDS];
+  const uint32_t part = blockIdx.x % S::PARTS, il = blockIdx.x / S::PARTS;
+  const uint32_t i = il / L, l = il % L;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const NttJob* jb = a.jobs + (size_t)i * 3 * L;
+  const uint32_t job = wv == 0 ? l : (wv == 1 ? 2 * L + l : L + l);
+  const LimbConst& lc = a.lc[l];
+  const BarrettConst bc = a.bc[l];
+  const size_t off = (size_t)l * S::N + ((size_t)part << 10) + lane;
+  uint64_t* shared_u = lds[1];
+  auto run = [&]<class A>() {
+    const A ar(lc);
+    typename A::V x[16];
+    row_fwd_regs<LOGN>(x, jb[job].dst, lc, ar, part, lds[wv]);
+    if (wv == 1) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) shared_u[lane + 64 * k] = ar.fwd_store(x[k]);
+    }
+    __syncthreads();
+    if (wv != 1) {
+      const GPtr<uint64_t> key = gld(pk + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
+      const GMut<uint64_t> out = gst(cts + (size_t)i * 2 * L * S::N + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint64_t u = shared_u[lane + 64 * k], p = key[64 * k];
+        uint64_t prod;
+        if constexpr (std::is_same_v<A, Fp64Arith>)
+          prod = f64_to_u64(mulmod_f64_any(u64_to_f64(p), u64_to_f64(u), lc.qd, lc.qinv));
+        else
+          prod = mulmod_barrett(p, u, bc);
+        out[64 * k] = addmod(prod, ar.fwd_store(x[k]), bc.q);
+      }
+    }
+  };
+  if (lc.fp64)
+    run.template operator()<Fp64Arith>();
+  else
+    run.template operator()<IntArith>();
+}
+
+template <int LOGN>
+static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk, uint64_t* cts,
+                                   hipStream_t s) {
+  using S = Split<LOGN>;
+  hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, NTT_LOAD_ENC, NTT_STORE_NONE>),
+                     dim3(ninputs * 3 * L * S::PARTS), dim3(64), 0, s, a);
+  hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * L * S::PARTS), dim3(192), 0, s, a, pk, cts, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+                                uint64_t* cts, hipStream_t s) {
+  switch (logn) {
+    case 13: return launch_encrypt_t<13>(a, ninputs, L, pk, cts, s);
+    case 14: return launch_encrypt_t<14>(a, ninputs, L, pk, cts, s);
+    case 15: return launch_encrypt_t<15>(a, ninputs, L, pk, cts, s);
     default: return hipErrorInvalidValue;
   }
 }

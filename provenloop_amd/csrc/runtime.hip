@@ -1712,8 +1712,16 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true));
     HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
                          ctx->d_stage_im, ctx->logn, L, st, z));
-    launch_jobs_ntt(ctx, false, set->d_enc_ntt, ni * 3 * L, NTT_LOAD_ENC);
-    HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
+    {
+      NttArgs ea{};
+      ea.lc = ctx->d_lc;
+      ea.jobs = set->d_enc_ntt;
+      ea.load = NTT_LOAD_ENC;
+      ea.bc = ctx->d_bc;
+      bool combined = false;
+      HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk->d, set->cts, &combined, st));
+      if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
+    }
     if (do_rescale) {
       // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
       NttArgs ia{}, fa{};

@@ -74,6 +74,13 @@ struct NttArgs {
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
+// The forward transforms of ninputs encrypt_pk inputs: a is the NTT_LOAD_ENC job
+// list (3L jobs per input, M_0..M_{L-1}, E1_0.., U_0..). At split sizes the
+// row passes also combine them with the public key pk = [b | a] into the
+// ciphertexts at cts + i 2 L N (*combined = true, k_encrypt_combine not needed);
+// otherwise the transforms are written to the jobs' dst and *combined = false.
+hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+                          uint64_t* cts, bool* combined, hipStream_t s);
 // The two transform launches of an evaluation-domain rescale: ninv inverse
 // transforms (inv, store NONE) of the products' last limbs, then nfwd forward
 // transforms (fwd, load REDUCE) of each last limb reduced modulo the lower
