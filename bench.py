@@ -323,7 +323,7 @@ def _timed_sessions(ctx, lora, sessions, dev_by_session, steps, warmup, seeds_fn
         for s, (pk, sk) in enumerate(sessions):
             dev_by_session[s].run(pk, sk, steps + w, seeds_fn(s, 10_000 + w))
     ctx.sync()
-    seeds = {(s, t): seeds_fn(s, t) for s in range(len(sessions)) for t in range(steps)}
+    seeds = {(s, t): np.asarray(seeds_fn(s, t), np.uint64) for s in range(len(sessions)) for t in range(steps)}
     t0 = time.perf_counter()
     for t in range(steps):
         for s, (pk, sk) in enumerate(sessions):
@@ -511,10 +511,11 @@ def main():
     for w in range(args.warmup):
         dev.run(pk, sk, args.steps + w, seeds_for(warm[w]))
     seeds = {t: seeds_for(t) for t in range(args.steps)}
+    seed_arr = {t: np.asarray(seeds[t], np.uint64) for t in range(args.steps)}  # prepared like the inputs
     ctx.sync()
     t0 = time.perf_counter()
     for t in range(args.steps):
-        dev.run(pk, sk, t, seeds[t])
+        dev.run(pk, sk, t, seed_arr[t])
         ctx.sync()  # one host synchronisation per token
     elapsed = time.perf_counter() - t0
     deltas_per_token = LAYERS * 2
@@ -523,7 +524,7 @@ def main():
     # the same tokens queued back to back (host launches overlap the GPU; one sync at the end)
     t2 = time.perf_counter()
     for t in range(args.steps):
-        dev.run(pk, sk, t, seeds[t])
+        dev.run(pk, sk, t, seed_arr[t])
     ctx.sync()
     piped = time.perf_counter() - t2
 

@@ -162,7 +162,7 @@ def device_count() -> int:
 
 
 def ptr(a: np.ndarray):
-    return a.ctypes.data_as(VP)
+    return VP(a.ctypes.data)  # half the cost of a.ctypes.data_as(VP) per call
 
 
 def handle_array(objs) -> C.Array:

@@ -234,11 +234,9 @@ hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeCons
   hipError_t e;
 #define TH_DEC(LP)                                                                                         \
   case LP:                                                                                                 \
-    e = hipFuncSetAttribute((const void*)k_decode_parts<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
-                            (int)lds_a);                                                                   \
+    e = allow_full_lds<k_decode_parts<LP>>();                                                              \
     if (e != hipSuccess) return e;                                                                         \
-    e = hipFuncSetAttribute((const void*)k_decode_final<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
-                            (int)lds_b);                                                                   \
+    e = allow_full_lds<k_decode_final<LP>>();                                                              \
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_decode_parts<LP>, dim3(1u << LP, njobs), dim3(DEC_THREADS), lds_a, s, jobs, dc,   \
                        twist_re, twist_im, stage_re, stage_im, logn);                                      \

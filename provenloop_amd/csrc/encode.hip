@@ -191,8 +191,7 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
   hipError_t e;
 #define TH_ENC(LP)                                                                                         \
   case LP:                                                                                                 \
-    e = hipFuncSetAttribute((const void*)k_encode_parts<LP>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
-                            (int)lds);                                                                     \
+    e = allow_full_lds<k_encode_parts<LP>>();                                                              \
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
                        stage_im, logn, z_base);                                                            \

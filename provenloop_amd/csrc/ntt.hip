@@ -316,13 +316,8 @@ static hipError_t launch_one(const NttArgs& a, uint32_t njobs, hipStream_t s) {
   const size_t lds = (size_t)S::LDS_ELEMS * 8;
   return with_ops<INV>(a.jobs ? a.load : NTT_LOAD_NONE, a.jobs ? a.store : NTT_STORE_NONE,
                   [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
-                    static bool attr_set = false;  // one per instantiation
-                    if (!attr_set) {
-                      hipError_t e = hipFuncSetAttribute((const void*)ntt_kernel<LOGN, INV, LD, ST>,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                      if (e != hipSuccess) return e;
-                      attr_set = true;
-                    }
+                    const hipError_t e = allow_full_lds<ntt_kernel<LOGN, INV, LD, ST>>();
+                    if (e != hipSuccess) return e;
                     hipLaunchKernelGGL((ntt_kernel<LOGN, INV, LD, ST>), dim3(njobs), dim3(S::T), lds, s, a);
                     return hipGetLastError();
                   });

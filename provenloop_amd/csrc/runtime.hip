@@ -156,6 +156,7 @@ void parallel_for(size_t count, F&& f) {
 struct th_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipEvent_t done = nullptr;  // recorded by wait_stream
   uint32_t N = 0, logn = 0, L = 0;
   std::vector<uint64_t> q;
   std::vector<LimbConst> h_lc;
@@ -300,6 +301,17 @@ th_ct* new_ct(th_ctx* c, uint32_t limbs, double scale) {
   th_ct* ct = new th_ct{c, limbs, scale, nullptr};
   ct->d = (uint64_t*)c->pool.get(2 * limbs * poly_bytes(c));
   return ct;
+}
+
+// Wait until everything queued on the context's stream has finished, polling
+// an event instead of blocking in the driver: the caller resumes within a
+// microsecond or so of the last kernel (a blocking wait is woken later), which
+// matters when the host synchronises once per token.
+void wait_stream(th_ctx* c) {
+  HIPCHK(hipEventRecord(c->done, c->stream));
+  hipError_t e;
+  while ((e = hipEventQuery(c->done)) == hipErrorNotReady) __builtin_ia32_pause();
+  HIPCHK(e);
 }
 
 void check_ct(th_ctx* c, const th_ct* ct) {
@@ -468,6 +480,7 @@ void destroy_ctx(th_ctx* c) {
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
   for (auto& kv : c->seg_p) (void)hipFree(kv.second);
+  if (c->done) (void)hipEventDestroy(c->done);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -942,6 +955,7 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       c->q = q;
       HIPCHK(hipSetDevice(device));
       HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      HIPCHK(hipEventCreateWithFlags(&c->done, hipEventDisableTiming));
       build_tables(c);
       c->ring.init(64u << 20);
     } catch (...) {
@@ -970,7 +984,7 @@ int th_ctx_sync(th_ctx* ctx) {
     need(ctx != nullptr, "null context");
     std::lock_guard<std::mutex> lk(ctx->mu);
     use_device(ctx);
-    HIPCHK(hipStreamSynchronize(ctx->stream));
+    wait_stream(ctx);
   });
 }
 
@@ -1754,12 +1768,12 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       char* hh = (char*)ctx->ring.reserve(db + ib, st);
       if (!deltas_on_device) HIPCHK(hipMemcpyAsync(hh, set->deltas, db, hipMemcpyDeviceToHost, st));
       if (inter) HIPCHK(hipMemcpyAsync(hh + db, set->sums, ib, hipMemcpyDeviceToHost, st));
-      HIPCHK(hipStreamSynchronize(st));
+      wait_stream(ctx);
       if (!deltas_on_device) memcpy(deltas, hh, db);
       if (inter) memcpy(inter, hh + db, ib);
     } else if (!hidden_on_device) {
       // the host input sits in the staging ring: finish reading it before returning
-      HIPCHK(hipStreamSynchronize(st));
+      wait_stream(ctx);
     }
   });
 }

@@ -72,6 +72,16 @@ struct NttArgs {
   uint32_t pad_;
 };
 
+// Lets kernel K use up to the whole 160 KiB of a CU's LDS as dynamic shared
+// memory. Set once per kernel (the first call's result is kept), so launches
+// on the per-token path do not repeat the driver call.
+template <auto K>
+hipError_t allow_full_lds() {
+  static const hipError_t e =
+      hipFuncSetAttribute((const void*)K, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return e;
+}
+
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
 // The forward transforms of ninputs encrypt_pk inputs: a is the NTT_LOAD_ENC job
