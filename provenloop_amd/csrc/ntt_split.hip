@@ -421,9 +421,10 @@ hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, con
 // transform (0: M, 1: U, 2: E1), each with its own LDS slice; U's wavefront
 // hands its canonical outputs to the other two through LDS, which form and
 // store c0 and c1. jobs: 3L per input (M_0..M_{L-1}, E1_0.., U_0..);
-// pk = [b (L) | a (L)]; input i's ciphertext at cts + i 2 L N.
+// pkp = [b (L) | a (L)] as prepared pairs (w, companion), so each product is
+// one Shoup or FP64 step; input i's ciphertext at cts + i 2 L N.
 template <int LOGN>
-__global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pk, uint64_t* cts, uint32_t L) {
+__global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pkp, uint64_t* cts, uint32_t L) {
   using S = Split<LOGN>;
   __shared__ uint64_t lds[3][S::LDS];
   const uint32_t part = blockIdx.x % S::PARTS, il = blockIdx.x / S::PARTS;
@@ -445,17 +446,24 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
     }
     __syncthreads();
     if (wv != 1) {
-      const GPtr<uint64_t> key = gld(pk + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
+      const GPtr<ShoupTw> key = gld(reinterpret_cast<const ShoupTw*>(pkp) + (wv == 0 ? 0 : (size_t)L * S::N) + off);
       const GMut<uint64_t> out = gst(cts + (size_t)i * 2 * L * S::N + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        const uint64_t u = shared_u[lane + 64 * k], p = key[64 * k];
-        uint64_t prod;
-        if constexpr (std::is_same_v<A, Fp64Arith>)
-          prod = f64_to_u64(mulmod_f64_any(u64_to_f64(p), u64_to_f64(u), lc.qd, lc.qinv));
-        else
-          prod = mulmod_barrett(p, u, bc);
-        out[64 * k] = addmod(prod, ar.fwd_store(x[k]), bc.q);
+        const uint64_t u = shared_u[lane + 64 * k], m = ar.fwd_store(x[k]);
+        const ShoupTw p = ld16(key, 64 * k);
+        uint64_t r;
+        if constexpr (std::is_same_v<A, Fp64Arith>) {
+          // (-q/2, q/2) + [0, q)
+          double t = mulmod_f64(u64_to_f64(u), u64_to_f64(p.w), __builtin_bit_cast(double, p.ws), lc.qd) +
+                     u64_to_f64(m);
+          t = t < 0.0 ? t + lc.qd : t;
+          r = f64_to_u64(t >= lc.qd ? t - lc.qd : t);
+        } else {
+          r = shoup_approx(u, p.w, p.ws, bc.q) + m;  // [0, 5q)
+          r = csub(csub(csub(r, 4 * bc.q), 2 * bc.q), bc.q);
+        }
+        out[64 * k] = r;
       }
     }
   };
@@ -466,12 +474,12 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
 }
 
 template <int LOGN>
-static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk, uint64_t* cts,
+static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp, uint64_t* cts,
                                    hipStream_t s) {
   using S = Split<LOGN>;
   hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, NTT_LOAD_ENC, NTT_STORE_NONE>),
                      dim3(ninputs * 3 * L * S::PARTS), dim3(64), 0, s, a);
-  hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * L * S::PARTS), dim3(192), 0, s, a, pk, cts, L);
+  hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * L * S::PARTS), dim3(192), 0, s, a, pkp, cts, L);
   return hipGetLastError();
 }
 

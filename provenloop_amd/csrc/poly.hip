@@ -60,6 +60,39 @@ __global__ void k_pt_sum(const uint64_t* __restrict__ src, uint64_t* __restrict_
   }
 }
 
+// Operands fixed for many products (keys) prepared as pairs in the twiddle
+// tables' formats: (w, floor(w 2^64 / q)) on the integer limbs, (w, w / q as
+// a double) on limbs below 2^41, so a product by w is one Shoup or one FP64
+// step instead of a 64-bit Barrett reduction. src: count x L x n residues;
+// dst: the same as 16-byte pairs.
+__device__ __forceinline__ uint64_t shoup_companion(uint64_t w, const BarrettConst& b) {
+  // w 2^64 r / 2^128 with r = floor((2^128 - 1) / q) is at most 1 short of
+  // floor(w 2^64 / q); the remainder w 2^64 - est q (< 2q) is exact mod 2^64
+  uint64_t est = w * b.r_hi + __umul64hi(w, b.r_lo);
+  uint64_t rem = (uint64_t)0 - est * b.q;
+  while (rem >= b.q) {
+    ++est;
+    rem -= b.q;
+  }
+  return est;
+}
+
+__global__ void k_prepare_pairs(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                const BarrettConst* __restrict__ bc, const LimbConst* __restrict__ lc, uint32_t n,
+                                uint32_t L, uint64_t total) {
+  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t l = (uint32_t)((e / n) % L);
+    const uint64_t w = src[e];
+    uint64_t c;
+    if (lc[l].fp64)
+      c = __builtin_bit_cast(uint64_t, (double)w / lc[l].qd);  // correctly rounded: both exact below 2^53
+    else
+      c = shoup_companion(w, bc[l]);
+    dst[2 * e] = w;
+    dst[2 * e + 1] = c;
+  }
+}
+
 // dst[l][i] = x[i] mod q_l for signed integer coefficients (encoding.rs:193-204).
 __global__ void k_signed_to_rns(const int64_t* __restrict__ x, uint64_t* __restrict__ dst,
                                 const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L) {
@@ -128,6 +161,15 @@ hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, 
   const uint64_t total = (uint64_t)nb * L * n;
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(k_pt_sum, dim3(blocks), dim3(256), 0, s, src, dst, q, k, nb, L, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_prepare_pairs(const uint64_t* src, uint64_t* dst, const BarrettConst* bc, const LimbConst* lc,
+                                uint32_t n, uint32_t L, uint32_t count, hipStream_t s) {
+  const uint64_t total = (uint64_t)count * L * n;
+  if (!total) return hipSuccess;
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_prepare_pairs, dim3(blocks), dim3(256), 0, s, src, dst, bc, lc, n, L, total);
   return hipGetLastError();
 }
 

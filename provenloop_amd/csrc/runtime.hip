@@ -183,7 +183,8 @@ struct th_sk {
 };
 struct th_pk {
   th_ctx* ctx;
-  uint64_t* d;  // [b | a], L x N each
+  uint64_t* d;                  // [b | a], L x N each
+  mutable uint64_t* dp = nullptr;  // the same as prepared pairs (launch_prepare_pairs), made on first use
 };
 struct th_ct {
   th_ctx* ctx;
@@ -312,6 +313,17 @@ void wait_stream(th_ctx* c) {
   hipError_t e;
   while ((e = hipEventQuery(c->done)) == hipErrorNotReady) __builtin_ia32_pause();
   HIPCHK(e);
+}
+
+// The public key as prepared pairs, made on the context's stream the first
+// time it is needed (queued before its first reader).
+const uint64_t* pk_pairs(th_ctx* c, const th_pk* pk) {
+  if (!pk->dp) {
+    uint64_t* p = (uint64_t*)c->pool.get(2 * 2 * (size_t)c->L * c->N * 8);
+    HIPCHK(launch_prepare_pairs(pk->d, p, c->d_bc, c->d_lc, c->N, c->L, 2, c->stream));
+    pk->dp = p;
+  }
+  return pk->dp;
 }
 
 void check_ct(th_ctx* c, const th_ct* ct) {
@@ -1056,6 +1068,7 @@ int th_sk_free(th_sk* sk) {
 int th_pk_free(th_pk* pk) {
   return guarded([&] {
     if (!pk) return;
+    if (pk->dp) pk->ctx->pool.put(pk->dp);
     pk->ctx->pool.put(pk->d);
     delete pk;
   });
@@ -1733,7 +1746,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       ea.load = NTT_LOAD_ENC;
       ea.bc = ctx->d_bc;
       bool combined = false;
-      HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk->d, set->cts, &combined, st));
+      HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk_pairs(ctx, pk), set->cts, &combined, st));
       if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
     }
     if (do_rescale) {

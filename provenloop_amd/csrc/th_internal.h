@@ -86,10 +86,11 @@ hipError_t allow_full_lds() {
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
 // The forward transforms of ninputs encrypt_pk inputs: a is the NTT_LOAD_ENC job
 // list (3L jobs per input, M_0..M_{L-1}, E1_0.., U_0..). At split sizes the
-// row passes also combine them with the public key pk = [b | a] into the
-// ciphertexts at cts + i 2 L N (*combined = true, k_encrypt_combine not needed);
-// otherwise the transforms are written to the jobs' dst and *combined = false.
-hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+// row passes also combine them with the public key, given as prepared pairs
+// pkp of [b | a] (launch_prepare_pairs), into the ciphertexts at
+// cts + i 2 L N (*combined = true, k_encrypt_combine not needed); otherwise
+// the transforms are written to the jobs' dst and *combined = false.
+hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
                           uint64_t* cts, bool* combined, hipStream_t s);
 // The two transform launches of an evaluation-domain rescale: ninv inverse
 // transforms (inv, store NONE) of the products' last limbs, then nfwd forward
