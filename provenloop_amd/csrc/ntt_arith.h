@@ -38,7 +38,7 @@ struct IntArith {
   // inverse GS butterfly, inputs/outputs in [0, 4q)
   __device__ __forceinline__ void inv(V& a, V& b, const Tw& t) const {
     const uint64_t X = a, Y = b;
-    a = csub(X + Y, four_q);
+    a = csub_n(X + Y, four_q, n4q());
     b = shoup_approx(X + four_q - Y, t.w, t.ws, q);
   }
   // last inverse stage with N^{-1} folded in; canonical outputs
