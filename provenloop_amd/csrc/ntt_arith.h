@@ -126,6 +126,8 @@ struct LoadOp {
       return sub == 0 ? csub(r + enc_residue((int64_t)gld(aux)[i]), bc.q) : r;
     }
     const uint64_t x = gld(src)[i];
+    if constexpr (LD == NTT_LOAD_MULM) return mont_mul(x, gld(aux)[i], bc);
+    if constexpr (LD == NTT_LOAD_DOTM) return x + mont_mul(gld(aux)[i], gld(key)[i], bc);
     if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
     if constexpr (LD == NTT_LOAD_REDUCE) return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
     if constexpr (LD == NTT_LOAD_DOT) return addmod(x, mulmod_barrett(gld(aux)[i], gld(key)[i], bc), bc.q);
@@ -210,13 +212,15 @@ template <uint32_t LD, uint32_t ST>
 __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint32_t limb, uint32_t n,
                                         LoadOp<LD>& op, StoreOp<ST>& so) {
   op.aux = jb.aux;
-  if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT || LD == NTT_LOAD_ENC) op.bc = a.bc[limb];
+  if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT || LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM ||
+                LD == NTT_LOAD_DOTM)
+    op.bc = a.bc[limb];
   if constexpr (LD == NTT_LOAD_ENC) {
     op.sub = jb.sub;
     op.qd = a.lc[limb].qd;
     op.qinv = a.lc[limb].qinv;
   }
-  if constexpr (LD == NTT_LOAD_DOT) op.key = a.key + (uint64_t)limb * n;
+  if constexpr (LD == NTT_LOAD_DOT || LD == NTT_LOAD_DOTM) op.key = a.key + (uint64_t)limb * n;
   if constexpr (LD == NTT_LOAD_REDUCE) op.rc = a.rc[limb];
   so.aux = jb.aux;
   so.aux2 = jb.aux2;
@@ -232,8 +236,8 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE | ENC,
-// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL | DOT,
-// NONE), (DOT, SEGSUM).
+// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL |
+// MULM | DOT, NONE), (DOT | DOTM, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   if constexpr (!INV) {
@@ -247,9 +251,12 @@ __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   } else {
     if (load == NTT_LOAD_DOT && store == NTT_STORE_SEGSUM)
       return f.template operator()<NTT_LOAD_DOT, NTT_STORE_SEGSUM>();
+    if (load == NTT_LOAD_DOTM && store == NTT_STORE_SEGSUM)
+      return f.template operator()<NTT_LOAD_DOTM, NTT_STORE_SEGSUM>();
     if (store != NTT_STORE_NONE) return hipErrorInvalidValue;
     if (load == NTT_LOAD_NONE) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_NONE>();
     if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_MULM) return f.template operator()<NTT_LOAD_MULM, NTT_STORE_NONE>();
     if (load == NTT_LOAD_DOT) return f.template operator()<NTT_LOAD_DOT, NTT_STORE_NONE>();
     return hipErrorInvalidValue;
   }

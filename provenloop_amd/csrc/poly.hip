@@ -93,6 +93,15 @@ __global__ void k_prepare_pairs(const uint64_t* __restrict__ src, uint64_t* __re
   }
 }
 
+// count x L x n residues into Montgomery form, w 2^64 mod q (mont_mul).
+__global__ void k_to_montgomery(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L, uint64_t total) {
+  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+    const BarrettConst& m = bc[(e / n) % L];
+    dst[e] = mulmod_barrett(src[e], m.r64, m);
+  }
+}
+
 // dst[l][i] = x[i] mod q_l for signed integer coefficients (encoding.rs:193-204).
 __global__ void k_signed_to_rns(const int64_t* __restrict__ x, uint64_t* __restrict__ dst,
                                 const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L) {
@@ -170,6 +179,15 @@ hipError_t launch_prepare_pairs(const uint64_t* src, uint64_t* dst, const Barret
   if (!total) return hipSuccess;
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(k_prepare_pairs, dim3(blocks), dim3(256), 0, s, src, dst, bc, lc, n, L, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_to_montgomery(const uint64_t* src, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
+                                uint32_t count, hipStream_t s) {
+  const uint64_t total = (uint64_t)count * L * n;
+  if (!total) return hipSuccess;
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_to_montgomery, dim3(blocks), dim3(256), 0, s, src, dst, bc, n, L, total);
   return hipGetLastError();
 }
 

@@ -69,6 +69,9 @@ hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_lim
 hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, uint32_t k, uint32_t nb, uint32_t L,
                          uint32_t n, hipStream_t s);
 // pk (optional): the public key [b | a] for every job instead of the jobs' fields.
+// count x L x n residues -> Montgomery form, w 2^64 mod q (k_to_montgomery).
+hipError_t launch_to_montgomery(const uint64_t* src, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
+                                uint32_t count, hipStream_t s);
 // count x L x n residues -> the same as (w, companion) pairs (k_prepare_pairs).
 hipError_t launch_prepare_pairs(const uint64_t* src, uint64_t* dst, const BarrettConst* bc, const LimbConst* lc,
                                 uint32_t n, uint32_t L, uint32_t count, hipStream_t s);

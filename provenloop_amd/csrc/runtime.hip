@@ -179,7 +179,8 @@ struct th_ctx {
 
 struct th_sk {
   th_ctx* ctx;
-  uint64_t* d;  // L x N, NTT domain
+  uint64_t* d;                     // L x N, NTT domain
+  mutable uint64_t* dm = nullptr;  // the same in Montgomery form (launch_to_montgomery), made on first use
 };
 struct th_pk {
   th_ctx* ctx;
@@ -207,6 +208,7 @@ struct th_lora {
   uint64_t n_deltas = 0;
   std::vector<void*> owned;
   uint64_t* pts = nullptr;     // n_batches x L x N, NTT domain
+  uint64_t* ptm = nullptr;     // the same in Montgomery form (launch_to_montgomery)
   double* hidden = nullptr;    // n_in x d
   uint8_t* u = nullptr;        // n_in x N
   int64_t *e0 = nullptr, *e1 = nullptr;
@@ -326,6 +328,16 @@ const uint64_t* pk_pairs(th_ctx* c, const th_pk* pk) {
   return pk->dp;
 }
 
+// The secret key in Montgomery form, made likewise.
+const uint64_t* sk_montgomery(th_ctx* c, const th_sk* sk) {
+  if (!sk->dm) {
+    uint64_t* p = (uint64_t*)c->pool.get((size_t)c->L * c->N * 8);
+    HIPCHK(launch_to_montgomery(sk->d, p, c->d_bc, c->N, c->L, 1, c->stream));
+    sk->dm = p;
+  }
+  return sk->dm;
+}
+
 void check_ct(th_ctx* c, const th_ct* ct) {
   need(ct != nullptr, "null ciphertext");
   need(ct->ctx == c, "ciphertext belongs to another context");
@@ -418,7 +430,9 @@ void build_tables(th_ctx* c) {
     lc.inv = (const char*)c->d_tables + (size_t)(2 * l + 1) * N * 16;
     lc.fp64 = fp ? 1 : 0;
     const u128 r = (~(u128)0) / q;
-    bc[l] = BarrettConst{q, (uint64_t)(r >> 64), (uint64_t)r};
+    uint64_t qi = 1;  // q^{-1} mod 2^64 by Newton's iteration (each step doubles the correct bits)
+    for (int it = 0; it < 6; ++it) qi *= 2 - q * qi;
+    bc[l] = BarrettConst{q, (uint64_t)(r >> 64), (uint64_t)r, (uint64_t)0 - qi, (uint64_t)(((u128)1 << 64) % q)};
   }
   HIPCHK(hipMemcpy(c->d_tables, host_tab.data(), tab_bytes, hipMemcpyHostToDevice));
   HIPCHK(hipMalloc(&c->d_lc, L * sizeof(LimbConst)));
@@ -686,10 +700,10 @@ void launch_dot_segsum(th_ctx* c, const NttJob* d_jobs, uint32_t n, const th_sk*
   NttArgs a{};
   a.lc = c->d_lc;
   a.jobs = d_jobs;
-  a.load = NTT_LOAD_DOT;
+  a.load = NTT_LOAD_DOTM;
   a.store = NTT_STORE_SEGSUM;
   a.bc = c->d_bc;
-  a.key = sk->d;
+  a.key = sk_montgomery(c, sk);
   a.segw = W;
   a.cols = cols;
   HIPCHK(launch_ntt((int)c->logn, true, a, n, c->stream));
@@ -1060,6 +1074,7 @@ int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, 
 int th_sk_free(th_sk* sk) {
   return guarded([&] {
     if (!sk) return;
+    if (sk->dm) sk->ctx->pool.put(sk->dm);
     sk->ctx->pool.put(sk->d);
     delete sk;
   });
@@ -1517,6 +1532,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   }
   // device memory
   set->pts = (uint64_t*)set->alloc(nb * L * P);
+  set->ptm = (uint64_t*)set->alloc(nb * L * P);
   set->hidden = (double*)set->alloc((size_t)ni * d * 8);
   set->u = (uint8_t*)set->alloc((size_t)ni * N);
   set->e0 = (int64_t*)set->alloc((size_t)ni * N * 8);
@@ -1552,6 +1568,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     queue_encode(sc, z, nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
     ntt_strided(c, false, dst, dst, nb * k * L, L);
     if (k > 1) HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
+    HIPCHK(launch_to_montgomery(set->pts, set->ptm, c->d_bc, N, L, nb, c->stream));
     HIPCHK(hipStreamSynchronize(c->stream));  // the scope's buffers return to the pool
   }
   // per-token job lists
@@ -1595,6 +1612,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   for (uint32_t bt = 0; bt < nb; ++bt) {
     const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
     const uint64_t* pt = set->pts + (size_t)bt * L * N;
+    const uint64_t* ptm = set->ptm + (size_t)bt * L * N;
     uint64_t* w = set->work + (size_t)bt * 2 * L * N;
     uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
     uint64_t* mm = set->m + (size_t)bt * 2 * N;
@@ -1604,7 +1622,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
       for (uint32_t comp = 0; comp < 2; ++comp) {
         const uint64_t* cc = ct + (size_t)comp * L * N;
         uint64_t* lc = w + (size_t)comp * N;
-        inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, pt + (size_t)(L - 1) * N, nullptr, L - 1, 0});
+        inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, ptm + (size_t)(L - 1) * N, nullptr, L - 1, 0});
         for (uint32_t l = 0; l + 1 < L; ++l)
           fwd.push_back(NttJob{lc, r + (size_t)(comp * Lr + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
       }
@@ -1755,7 +1773,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       ia.lc = fa.lc = ctx->d_lc;
       ia.bc = fa.bc = ctx->d_bc;
       ia.jobs = set->d_inv_mul;
-      ia.load = NTT_LOAD_MUL;
+      ia.load = NTT_LOAD_MULM;
       fa.jobs = set->d_fwd_rs;
       fa.load = NTT_LOAD_REDUCE;
       fa.store = NTT_STORE_MUL_RESCALE;

@@ -125,6 +125,8 @@ __device__ __forceinline__ uint64_t shoup_approx(uint64_t x, uint64_t w, uint64_
 struct BarrettConst {
   uint64_t q;
   uint64_t r_hi, r_lo;  // floor((2^128 - 1) / q) as two words
+  uint64_t mq;          // -q^{-1} mod 2^64 (Montgomery products)
+  uint64_t r64;         // 2^64 mod q (into Montgomery form)
 };
 
 __device__ __forceinline__ uint64_t mulmod_barrett(uint64_t a, uint64_t b, const BarrettConst& m) {
@@ -143,6 +145,17 @@ __device__ __forceinline__ uint64_t mulmod_barrett(uint64_t a, uint64_t b, const
 }
 
 __device__ __forceinline__ uint64_t addmod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
+
+// Montgomery product a * b * 2^-64 mod q in [0, 2q) for any 64-bit a and
+// b < q: with T = a b and m = T mod 2^64 * (-q^{-1}) mod 2^64, T + m q is a
+// multiple of 2^64, its low words cancel (a carry exactly when T mod 2^64 is
+// nonzero), and (T + m q) / 2^64 < 2q. With b = w 2^64 mod q (w in Montgomery
+// form) this is a * w mod q, in about half the multiplies of a Barrett product.
+__device__ __forceinline__ uint64_t mont_mul(uint64_t a, uint64_t b, const BarrettConst& m) {
+  const uint64_t t_lo = a * b, t_hi = __umul64hi(a, b);
+  const uint64_t k = t_lo * m.mq;
+  return t_hi + __umul64hi(k, m.q) + (t_lo != 0 ? 1 : 0);
+}
 
 // e >= 0 ? e mod q : q - (|e| mod q) (ciphertext.rs:132-136, :275-287; encoding.rs:198-202)
 __device__ __forceinline__ uint64_t signed_residue_dev(int64_t e, const BarrettConst& m) {

@@ -20,7 +20,17 @@ namespace th {
 //            0: x = (m + e0) mod q, src = m, aux = e0 (i64 coefficients)
 //            1: x = e1 mod q, src = e1 (i64)
 //            2: x = u mapped 0 -> q-1, 1 -> 0, 2 -> 1, src = u (u8)
-enum NttLoad : uint32_t { NTT_LOAD_NONE = 0, NTT_LOAD_MUL = 1, NTT_LOAD_REDUCE = 2, NTT_LOAD_DOT = 3, NTT_LOAD_ENC = 4 };
+//   MULM     MUL with aux in Montgomery form (launch_to_montgomery); x in [0, 2q)
+//   DOTM     DOT with the key in Montgomery form; x in [0, 3q)
+enum NttLoad : uint32_t {
+  NTT_LOAD_NONE = 0,
+  NTT_LOAD_MUL = 1,
+  NTT_LOAD_REDUCE = 2,
+  NTT_LOAD_DOT = 3,
+  NTT_LOAD_ENC = 4,
+  NTT_LOAD_MULM = 5,
+  NTT_LOAD_DOTM = 6
+};
 
 // Operation applied to every output of a FORWARD transform before it is
 // stored (fused consumer), y = the transformed value in [0, q):
