@@ -6,7 +6,9 @@
 //   coeff_j = (a_re_j / N) * cos(pi j/N) + (a_im_j / N) * sin(pi j/N)
 //   m_j = round(coeff_j * 2^40) as i64 (half away from zero, saturating)
 // then per limb l:  M_l = (m + e0) mod q_l,  E1_l = e1 mod q_l,  U_l = u mod q_l
-// which the forward NTT and the combine kernel turn into the ciphertext.
+// which the forward NTT and the combine kernel turn into the ciphertext. A
+// job with mvals set writes m itself instead (the LoRA set's token pass: its
+// encrypt transforms form the residues as they load, NTT_LOAD_ENC).
 // All f64 steps round exactly as on the host (-ffp-contract=off, host
 // twiddles), so m is bit-identical to the reference encoder's.
 #include "encode_sample.h"
