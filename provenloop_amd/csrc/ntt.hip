@@ -49,7 +49,7 @@ constexpr int NTT_WHOLE_MAX_LOGN = 14;
 hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
 hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf,
                                 hipStream_t s);
-hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
                                 uint64_t* cts, hipStream_t s);
 
 template <int LOGN>
@@ -338,13 +338,13 @@ hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const Ntt
   return launch_ntt(logn, false, fwd, nfwd, s);
 }
 
-hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
                           uint64_t* cts, bool* combined, hipStream_t s) {
   *combined = false;
   if (ninputs == 0) return hipSuccess;
   if (use_split(logn, ninputs * 3 * L) && a.jobs && a.load == NTT_LOAD_ENC && a.store == NTT_STORE_NONE) {
     *combined = true;
-    return launch_encrypt_split(logn, a, ninputs, L, pk, cts, s);
+    return launch_encrypt_split(logn, a, ninputs, L, pkp, cts, s);
   }
   return launch_ntt(logn, false, a, ninputs * 3 * L, s);
 }

@@ -483,12 +483,12 @@ static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t 
   return hipGetLastError();
 }
 
-hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pk,
+hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
                                 uint64_t* cts, hipStream_t s) {
   switch (logn) {
-    case 13: return launch_encrypt_t<13>(a, ninputs, L, pk, cts, s);
-    case 14: return launch_encrypt_t<14>(a, ninputs, L, pk, cts, s);
-    case 15: return launch_encrypt_t<15>(a, ninputs, L, pk, cts, s);
+    case 13: return launch_encrypt_t<13>(a, ninputs, L, pkp, cts, s);
+    case 14: return launch_encrypt_t<14>(a, ninputs, L, pkp, cts, s);
+    case 15: return launch_encrypt_t<15>(a, ninputs, L, pkp, cts, s);
     default: return hipErrorInvalidValue;
   }
 }
