@@ -234,6 +234,29 @@ def test_lora_set_argument_errors(env):
     _check(got, got_sums, exp, exp_sums)
 
 
+def test_lora_set_split_sizes_n8192():
+    """N = 8192 with 24 inputs: 288 encrypt transforms, past the whole-polynomial kernel's batch,
+    so the encrypt residues and the public-key combine run in the split kernels at log N = 13;
+    every input's segment sums equal th_lora_a_pass's (unfused encrypt) bit for bit, and two
+    inputs match the oracle."""
+    eng, ref = tensafe_he.CkksContext(8192), orc.Context(8192)
+    sk, rsk = eng.keygen(seed=5), ref.keygen(5)
+    pk, rpk = eng.keygen_public(sk, seed=6), ref.keygen_public(rsk, 6)
+    rng = np.random.default_rng(81)
+    n_in, d = 24, 512
+    H = rng.normal(size=(n_in, d)) * 0.1
+    proj = _projections(rng, n_in, d, ranks=[8] * n_in, d_outs=[16] * n_in)
+    ls = zero_moai.LoraSet(eng, n_in, proj)
+    assert ls.cols == 8 and ls.n_batches == n_in
+    seeds = list(range(300, 300 + n_in))
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    pts = [eng.encode_to_ntt(p) for _, A, _ in proj for p in zero_moai.pack_rows(A, 4096)]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, list(range(n_in))), got_sums)
+    for i in (0, n_in - 1):
+        exp, exp_sums = _oracle(ref, rpk, rsk, H[i:i + 1], seeds[i:i + 1], [(0, proj[i][1], proj[i][2])], True)
+        _check(got[i:i + 1], got_sums[i:i + 1], exp, exp_sums)
+
+
 def test_lora_set_crt_branch_after_rescale():
     """A chain whose last prime is 30-bit: the rescaled scale is ~2^50 > 1.5 * 2^40, so the
     decrypt takes the CRT branch over limbs 0 and 1 (ciphertext.rs:351)."""
