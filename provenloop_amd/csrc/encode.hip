@@ -11,8 +11,8 @@
 // encrypt transforms form the residues as they load, NTT_LOAD_ENC).
 // All f64 steps round exactly as on the host (-ffp-contract=off, host
 // twiddles), so m is bit-identical to the reference encoder's.
-#include "encode_sample.h"
 #include "fft_device.h"
+#include "sample_device.h"
 
 namespace th {
 
@@ -22,7 +22,9 @@ template <int LP>
 __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* __restrict__ jobs,
                                                               const double* __restrict__ stage_re,
                                                               const double* __restrict__ stage_im, uint32_t logn,
-                                                              const double* __restrict__ z_base) {
+                                                              const double* __restrict__ z_base,
+                                                              const SampleJob* __restrict__ fix, SeedBlock sb,
+                                                              int use_sb, int force_serial) {
   extern __shared__ double sh[];
   const uint32_t n = 1u << logn, S = n / 2;
   const uint32_t M = n >> LP;
@@ -86,6 +88,11 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
     out[i] = re[fft_pad(i)];
     out[M + i] = im[fft_pad(i)];
+  }
+  // the sampler launch queued before this one left its rejection check here
+  if (fix && part == 0 && threadIdx.x == 0) {
+    const SampleJob sj = fix[blockIdx.y];
+    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial);
   }
 }
 
@@ -176,8 +183,13 @@ size_t encode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s, const double* z_base) {
+                         uint32_t L, hipStream_t s, const double* z_base, const SampleJob* fix, const uint64_t* seeds,
+                         int force_serial) {
   if (!njobs) return hipSuccess;
+  if (fix && njobs > SEEDS_PER_LAUNCH) return hipErrorInvalidValue;
+  SeedBlock sb{};
+  if (fix && seeds)
+    for (uint32_t i = 0; i < njobs; ++i) sb.v[i] = seeds[i];
   // at least one part per LDS budget; more parts (up to 16, of at least 1024
   // values) while the batch would leave CUs idle: the parts are independent
   // workgroups and the result is the same for any split
@@ -196,7 +208,7 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
     e = allow_full_lds<k_encode_parts<LP>>();                                                              \
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
-                       stage_im, logn, z_base);                                                            \
+                       stage_im, logn, z_base, fix, sb, (int)(seeds != nullptr), force_serial);            \
     hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im, \
                        stage_re, stage_im, logn, L);                                                       \
     return hipGetLastError();

@@ -17,12 +17,20 @@ struct EncodeJob {
   double* parts;       // scratch, encode_parts_doubles(logn) doubles
 };
 
+struct SampleJob;
+// Seeds travel with a sampler launch for up to this many jobs.
+constexpr uint32_t SEEDS_PER_LAUNCH = 64;
+
 // Encode z and write the per-limb residues of m (+ e0), e1 and u. With
 // z_base, job i reads its input at z_base + i * (rep_d, or N/2 without
-// replication) instead of its z field.
+// replication) instead of its z field. With fix (the sample jobs of a
+// flagged launch_sample_pk queued just before with fix_later, one per encode
+// job, at most SEEDS_PER_LAUNCH of them, and the same seeds), the launch also
+// finishes the sampler's rejection handling (k_sample_fix's work).
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s, const double* z_base = nullptr);
+                         uint32_t L, hipStream_t s, const double* z_base = nullptr, const SampleJob* fix = nullptr,
+                         const uint64_t* seeds = nullptr, int force_serial = 0);
 size_t encode_parts_doubles(uint32_t logn);
 
 struct SampleJob {
@@ -41,6 +49,6 @@ struct SampleJob {
 // of them) skip the re-derivation pass: the block kernel raises the flag and
 // only flagged jobs are replayed; the flag is cleared again.
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
-                            const uint64_t* seeds = nullptr, bool flagged = false);
+                            const uint64_t* seeds = nullptr, bool flagged = false, bool fix_later = false);
 
 }  // namespace th

@@ -1754,9 +1754,13 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       z = set->hidden;
     }
     // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true));
+    // the encoder launch (next on the stream) finishes the sampler's rejection
+    // check when every input's seed fits one launch
+    const bool fix_in_encode = ni <= SEEDS_PER_LAUNCH;
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, fix_in_encode));
     HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                         ctx->d_stage_im, ctx->logn, L, st, z));
+                         ctx->d_stage_im, ctx->logn, L, st, z, fix_in_encode ? set->d_sample : nullptr, seeds,
+                         ctx->force_serial));
     {
       NttArgs ea{};
       ea.lc = ctx->d_lc;
