@@ -42,19 +42,35 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   constexpr bool TWL = LP >= 3;
   const double* twr = stage_re;
   const double* twi = stage_im;
+  // 8 entries of each table per thread per round (one round with
+  // blockDim.x = M / 8), all loads issued before the first LDS store
+  constexpr int FV = 8;
   if constexpr (TWL) {
     double* tr = sh + 2 * MP;
     double* ti = sh + 2 * MP + M;
-    for (uint32_t i = threadIdx.x; i + 1 < M; i += blockDim.x) {
-      tr[i] = gld(stage_re)[i];
-      ti[i] = gld(stage_im)[i];
+    for (uint32_t i0 = threadIdx.x; i0 + 1 < M; i0 += FV * blockDim.x) {
+      double a[FV], b[FV];
+#pragma unroll
+      for (int e = 0; e < FV; ++e) {
+        const uint32_t i = i0 + e * blockDim.x;
+        const uint32_t ic = i + 1 < M ? i : 0;
+        a[e] = gld(stage_re)[ic];
+        b[e] = gld(stage_im)[ic];
+      }
+#pragma unroll
+      for (int e = 0; e < FV; ++e) {
+        const uint32_t i = i0 + e * blockDim.x;
+        if (i + 1 < M) {
+          tr[i] = a[e];
+          ti[i] = b[e];
+        }
+      }
     }
     twr = tr;
     twi = ti;
   }
   // input gather, 8 values per thread per round: all loads issued before the
   // first LDS store
-  constexpr int FV = 8;
   for (uint32_t j0 = threadIdx.x; j0 < M; j0 += FV * blockDim.x) {
     double v[FV];
 #pragma unroll
@@ -85,9 +101,23 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   __syncthreads();
   dit_stages_reg<true>(re, im, lb, twr, twi);
   const GMut<double> out = gst(jb.parts) + (size_t)part * 2 * M;
-  for (uint32_t i = threadIdx.x; i < M; i += blockDim.x) {
-    out[i] = re[fft_pad(i)];
-    out[M + i] = im[fft_pad(i)];
+  for (uint32_t i0 = threadIdx.x; i0 < M; i0 += FV * blockDim.x) {
+    double a[FV], b[FV];
+#pragma unroll
+    for (int e = 0; e < FV; ++e) {
+      const uint32_t i = i0 + e * blockDim.x;
+      const uint32_t ic = fft_pad(i < M ? i : 0);
+      a[e] = re[ic];
+      b[e] = im[ic];
+    }
+#pragma unroll
+    for (int e = 0; e < FV; ++e) {
+      const uint32_t i = i0 + e * blockDim.x;
+      if (i < M) {
+        out[i] = a[e];
+        out[M + i] = b[e];
+      }
+    }
   }
   // the sampler launch queued before this one left its rejection check here
   if (fix && part == 0 && threadIdx.x == 0) {
