@@ -12,9 +12,10 @@ __global__ __launch_bounds__(256) void k_lora_b(const LoraBJob* __restrict__ job
   const LoraBJob jb = jobs[blockIdx.y];
   const double* seg = sums + (size_t)jb.first_row * cols;  // batch-major: seg[b * cols + c]
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < jb.d_out; i += gridDim.x * blockDim.x) {
-    const double* brow = jb.b + (size_t)i * jb.rank;
+    const double* bcol = jb.b + i;  // rank-major: consecutive lanes read consecutive doubles
     double acc = 0.0;
-    for (uint32_t r = 0; r < jb.rank; ++r) acc = __fma_rn(brow[r], seg[r], acc);
+#pragma unroll 8
+    for (uint32_t r = 0; r < jb.rank; ++r) acc = __fma_rn(bcol[(size_t)r * jb.d_out], seg[r], acc);
     out[jb.out_off + i] = acc;
   }
 }

@@ -50,7 +50,7 @@ struct DecodeJob {
 // (batches of one projection are consecutive), which is the ZeRo-MOAI
 // extraction order (inference_engine.py:1379-1386).
 struct LoraBJob {
-  const double* b;     // d_out x rank, row-major
+  const double* b;     // B (d_out x rank) stored rank-major: element (i, r) at r * d_out + i
   uint32_t d_out;
   uint32_t rank;
   uint32_t first_row;  // first plaintext batch of the projection

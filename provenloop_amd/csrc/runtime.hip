@@ -1507,17 +1507,21 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
       batch_input.push_back(input_of[j]);
     }
     const size_t bn = (size_t)d_out[j] * ranks[j];
-    if (!gates) {
-      bmat.insert(bmat.end(), b[j], b[j] + bn);
-    } else {
-      std::vector<double> mix(bn, 0.0);
+    std::vector<double> mix(b[j], b[j] + bn);
+    if (gates) {
+      std::fill(mix.begin(), mix.end(), 0.0);
       for (uint32_t x = 0; x < k; ++x) {
         const double g = gates[(size_t)j * k + x];
         const double* bx = b[(size_t)j * k + x];
         for (size_t t = 0; t < bn; ++t) mix[t] += g * bx[t];
       }
-      bmat.insert(bmat.end(), mix.begin(), mix.end());
     }
+    // rank-major on the device (element (i, r) at r * d_out + i): the
+    // kernel's lanes, one output row each, then read consecutive addresses
+    const size_t b0 = bmat.size();
+    bmat.resize(b0 + bn);
+    for (uint32_t i = 0; i < d_out[j]; ++i)
+      for (uint32_t r = 0; r < ranks[j]; ++r) bmat[b0 + (size_t)r * d_out[j] + i] = mix[(size_t)i * ranks[j] + r];
     out_off += d_out[j];
     set->max_d_out = std::max(set->max_d_out, d_out[j]);
   }
