@@ -244,12 +244,18 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
       double acc[MAXC];
 #pragma unroll
       for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
+      // the weights of element k + PF are requested while element k is summed
+      constexpr int PF = S::E < 4 ? S::E : 4;
+      D2 wq[PF];
+      __builtin_amdgcn_sched_barrier(0);  // keep the requests after the last pass (register peak)
+#pragma unroll
+      for (int k = 0; k < PF; ++k) wq[k] = W[elem<S::LE, END>(tid, k)];
 #pragma unroll
       for (int k = 0; k < S::E; ++k) {
-        const uint32_t j = elem<S::LE, END>(tid, k);
         const uint64_t m = ar.inv_store(x[k]);
         const double v = m > half ? -(double)(q - m) : (double)m;
-        const D2 p = W[j];  // W_0[j], 2 cos(2 phi_j)
+        const D2 p = wq[k % PF];  // W_0[j], 2 cos(2 phi_j) at j = elem(tid, k)
+        if (k + PF < S::E) wq[k % PF] = W[elem<S::LE, END>(tid, k + PF)];
         double wp = p.x, wc = p.x;
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
