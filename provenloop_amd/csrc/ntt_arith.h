@@ -116,6 +116,18 @@ struct LoadOp {
     }
     return e >= 0 ? r : bc.q - r;
   }
+  // MULM in two steps, so that a pass can issue every element's operand
+  // loads before the first product: fetch reads (ct, pt) at position i,
+  // finish forms the product.
+  static constexpr uint32_t kind = LD;
+  struct Raw {
+    uint64_t x, a;
+  };
+  __device__ __forceinline__ Raw fetch(const uint64_t* src, uint32_t i) const {
+    static_assert(LD == NTT_LOAD_MULM, "two-step loads are for MULM");
+    return Raw{gld(src)[i], gld(aux)[i]};
+  }
+  __device__ __forceinline__ uint64_t finish(const Raw& r) const { return mont_mul(r.x, r.a, bc); }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
     if constexpr (LD == NTT_LOAD_ENC) {
       if (sub == 2) {

@@ -259,8 +259,18 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so.apply_prep(ar, x[k], c[NP > 1 ? k : 0]);
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
+    if constexpr (LOp::kind == NTT_LOAD_MULM) {
+      // all 32 operand loads in flight before the first product
+      typename LOp::Raw r[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
+      for (int k = 0; k < 16; ++k) r[k] = op.fetch(src, jbase + g(k));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(op.finish(r[k]));
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
+    }
     wave_exchange(x, lds, g, p2);
     inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
     wave_exchange(x, lds, p2, p1);
