@@ -116,18 +116,48 @@ struct LoadOp {
     }
     return e >= 0 ? r : bc.q - r;
   }
-  // MULM in two steps, so that a pass can issue every element's operand
-  // loads before the first product: fetch reads (ct, pt) at position i,
-  // finish forms the product.
+  // MULM and ENC in two steps, so that a pass issues all 16 of a thread's
+  // operand loads before any arithmetic (the per-element branches of the
+  // residue forms would otherwise hold each load until the previous
+  // element's result): fetch16 reads the operands of positions idx(0..15),
+  // finish forms one position's value. MULM reads (ct, pt); ENC, by the
+  // job's variant, the ternary byte (2), m or e1 (1), or m and e0 (0).
   static constexpr uint32_t kind = LD;
   struct Raw {
     uint64_t x, a;
   };
-  __device__ __forceinline__ Raw fetch(const uint64_t* src, uint32_t i) const {
-    static_assert(LD == NTT_LOAD_MULM, "two-step loads are for MULM");
-    return Raw{gld(src)[i], gld(aux)[i]};
+  template <class Idx>
+  __device__ __forceinline__ void fetch16(const uint64_t* src, const Idx& idx, Raw (&r)[16]) const {
+    static_assert(LD == NTT_LOAD_MULM || LD == NTT_LOAD_ENC, "two-step loads are for MULM and ENC");
+    const GPtr<uint64_t> s = gld(src);
+    if constexpr (LD == NTT_LOAD_ENC) {
+      if (sub == 2) {
+        const GPtr<uint8_t> u = gld(reinterpret_cast<const uint8_t*>(src));
+#pragma unroll
+        for (int k = 0; k < 16; ++k) r[k] = Raw{u[idx(k)], 0};
+      } else if (sub == 0) {
+        const GPtr<uint64_t> e = gld(aux);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) r[k] = Raw{s[idx(k)], e[idx(k)]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) r[k] = Raw{s[idx(k)], 0};
+      }
+    } else {
+      const GPtr<uint64_t> a = gld(aux);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) r[k] = Raw{s[idx(k)], a[idx(k)]};
+    }
   }
-  __device__ __forceinline__ uint64_t finish(const Raw& r) const { return mont_mul(r.x, r.a, bc); }
+  __device__ __forceinline__ uint64_t finish(const Raw& r) const {
+    if constexpr (LD == NTT_LOAD_ENC) {
+      if (sub == 2) return r.x == 0 ? bc.q - 1 : (r.x == 1 ? 0 : 1);
+      const uint64_t v = enc_residue((int64_t)r.x);
+      return sub == 0 ? csub(v + enc_residue((int64_t)r.a), bc.q) : v;
+    } else {
+      return mont_mul(r.x, r.a, bc);
+    }
+  }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
     if constexpr (LD == NTT_LOAD_ENC) {
       if (sub == 2) {

@@ -180,8 +180,17 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
   const A ar(lc);
   typename A::V x[16];
   if constexpr (!INV) {
+    if constexpr (LOp::kind == NTT_LOAD_ENC) {
+      // every operand load in flight before the first residue
+      typename LOp::Raw r[16];
+      op.fetch16(src, [&](int k) { return m.j1(k); }, r);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, m.j1(k)));
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(op.finish(r[k]));
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, m.j1(k)));
+    }
     column_fwd_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
   } else {
     column_inv_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
@@ -262,8 +271,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     if constexpr (LOp::kind == NTT_LOAD_MULM) {
       // all 32 operand loads in flight before the first product
       typename LOp::Raw r[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) r[k] = op.fetch(src, jbase + g(k));
+      op.fetch16(src, [&](int k) { return jbase + g(k); }, r);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op.finish(r[k]));
