@@ -458,18 +458,25 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
     const A ar(lc);
     typename A::V x[16];
     row_fwd_regs<LOGN>(x, jb[job].dst, lc, ar, part, lds[wv]);
+    // the key pairs are requested before the barrier, so their latency
+    // overlaps U's hand-over
+    ShoupTw kp[16];
+    if (wv != 1) {
+      const GPtr<ShoupTw> key = gld(reinterpret_cast<const ShoupTw*>(pkp) + (wv == 0 ? 0 : (size_t)L * S::N) + off);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) kp[k] = ld16(key, 64 * k);
+    }
     if (wv == 1) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) shared_u[lane + 64 * k] = ar.fwd_store(x[k]);
     }
     __syncthreads();
     if (wv != 1) {
-      const GPtr<ShoupTw> key = gld(reinterpret_cast<const ShoupTw*>(pkp) + (wv == 0 ? 0 : (size_t)L * S::N) + off);
       const GMut<uint64_t> out = gst(cts + (size_t)i * 2 * L * S::N + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const uint64_t u = shared_u[lane + 64 * k], m = ar.fwd_store(x[k]);
-        const ShoupTw p = ld16(key, 64 * k);
+        const ShoupTw p = kp[k];
         uint64_t r;
         if constexpr (std::is_same_v<A, Fp64Arith>) {
           // (-q/2, q/2) + [0, q)
