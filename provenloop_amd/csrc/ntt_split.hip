@@ -57,19 +57,36 @@ struct Split {
 __device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
 
 // Forward stages BHI down to BLO on registers that hold index bits
-// [EB, EB + 4); f = index of register 0 (its register bits are zero).
-template <int LOGN, int EB, int BHI, int BLO, class A>
+// [EB, EB + 4); f = index of register 0 (its register bits are zero). With
+// BATCH, each stage's twiddles (16 >> (rb + 1) of them) are all requested
+// before its first butterfly, for kernels whose register pressure otherwise
+// leads the scheduler to wait on each twiddle in turn.
+template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = false>
 __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar) {
 #pragma unroll
   for (int b = BHI; b >= BLO; --b) {
     const int rb = b - EB;
     const uint32_t base = ((1u << LOGN) | f) >> (b + 1);
+    if constexpr (BATCH) {
+      constexpr int NT = 16 >> 1;
+      typename A::Tw t[NT];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (k & (1 << rb)) continue;
-      const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
-      ar.fwd(x[k], x[k | (1 << rb)], t);
+      for (int j = 0; j < NT; ++j)
+        if (j < (16 >> (rb + 1))) t[j] = ld16(tw, base | (uint32_t)j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k & (1 << rb)) continue;
+        ar.fwd(x[k], x[k | (1 << rb)], t[k >> (rb + 1)]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k & (1 << rb)) continue;
+        const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
+        ar.fwd(x[k], x[k | (1 << rb)], t);
+      }
     }
   }
 }
@@ -143,16 +160,16 @@ struct ColumnMap {
 
 // Forward column pass on coefficients already in registers (Q1 layout, the
 // arithmetic's representation); writes the intermediate to dst (Q2).
-template <int LOGN, class A>
+template <int LOGN, class A, bool BATCH = false>
 __device__ __forceinline__ void column_fwd_regs(typename A::V (&x)[16], uint64_t* dst, const LimbConst& lc,
                                                 const ColumnMap<LOGN>& m, const A& ar, uint64_t* lds_raw) {
   constexpr int CB = Split<LOGN>::CB;
   const GMut<uint64_t> gdst = gst(dst);
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
-  fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4>(x, m.j1(0), tw, ar);
+  fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4, A, BATCH>(x, m.j1(0), tw, ar);
   wave_exchange(x, lds, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
-  fwd_stages<LOGN, CB, LOGN - 5, CB>(x, m.j2(0), tw, ar);
+  fwd_stages<LOGN, CB, LOGN - 5, CB, A, BATCH>(x, m.j2(0), tw, ar);
 #pragma unroll
   for (int k = 0; k < 16; ++k) gdst[m.j2(k)] = ar.raw(x[k]);
 }
@@ -388,13 +405,13 @@ __global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs
       Fp64Arith::V x[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = reduce_u64_f64(c[k], rc);
-      column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
+      column_fwd_regs<LOGN, Fp64Arith, true>(x, fj.dst, lcf, m, ar, lds);
     } else {
       const IntArith ar(lcf);
       IntArith::V x[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b);
-      column_fwd_regs<LOGN>(x, fj.dst, lcf, m, ar, lds);
+      column_fwd_regs<LOGN, IntArith, true>(x, fj.dst, lcf, m, ar, lds);
     }
   }
 }
