@@ -156,7 +156,6 @@ void parallel_for(size_t count, F&& f) {
 struct th_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t done = nullptr;  // recorded by wait_stream
   uint32_t N = 0, logn = 0, L = 0;
   std::vector<uint64_t> q;
   std::vector<LimbConst> h_lc;
@@ -306,14 +305,13 @@ th_ct* new_ct(th_ctx* c, uint32_t limbs, double scale) {
   return ct;
 }
 
-// Wait until everything queued on the context's stream has finished, polling
-// an event instead of blocking in the driver: the caller resumes within a
-// microsecond or so of the last kernel (a blocking wait is woken later), which
-// matters when the host synchronises once per token.
+// Wait until everything queued on the context's stream, by this library or
+// by a caller through th_ctx_stream, has finished. The stream is polled: no
+// marker is queued, and the caller resumes within a microsecond or so of the
+// last kernel, which matters when the host synchronises once per token.
 void wait_stream(th_ctx* c) {
-  HIPCHK(hipEventRecord(c->done, c->stream));
   hipError_t e;
-  while ((e = hipEventQuery(c->done)) == hipErrorNotReady) __builtin_ia32_pause();
+  while ((e = hipStreamQuery(c->stream)) == hipErrorNotReady) __builtin_ia32_pause();
   HIPCHK(e);
 }
 
@@ -506,7 +504,6 @@ void destroy_ctx(th_ctx* c) {
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
   for (auto& kv : c->seg_p) (void)hipFree(kv.second);
-  if (c->done) (void)hipEventDestroy(c->done);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -981,7 +978,6 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       c->q = q;
       HIPCHK(hipSetDevice(device));
       HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-      HIPCHK(hipEventCreateWithFlags(&c->done, hipEventDisableTiming));
       build_tables(c);
       c->ring.init(64u << 20);
     } catch (...) {
