@@ -126,6 +126,16 @@ struct LoadOp {
   struct Raw {
     uint64_t x, a;
   };
+  __device__ __forceinline__ Raw fetch(const uint64_t* src, uint32_t i) const {
+    static_assert(LD == NTT_LOAD_MULM || LD == NTT_LOAD_ENC, "two-step loads are for MULM and ENC");
+    if constexpr (LD == NTT_LOAD_ENC) {
+      if (sub == 2) return Raw{gld(reinterpret_cast<const uint8_t*>(src))[i], 0};
+      return Raw{gld(src)[i], sub == 0 ? gld(aux)[i] : 0};
+    } else {
+      return Raw{gld(src)[i], gld(aux)[i]};
+    }
+  }
+  // the variant test outside the element loop, so the 16 requests issue together
   template <class Idx>
   __device__ __forceinline__ void fetch16(const uint64_t* src, const Idx& idx, Raw (&r)[16]) const {
     static_assert(LD == NTT_LOAD_MULM || LD == NTT_LOAD_ENC, "two-step loads are for MULM and ENC");
@@ -159,16 +169,8 @@ struct LoadOp {
     }
   }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
-    if constexpr (LD == NTT_LOAD_ENC) {
-      if (sub == 2) {
-        const uint8_t u = gld(reinterpret_cast<const uint8_t*>(src))[i];
-        return u == 0 ? bc.q - 1 : (u == 1 ? 0 : 1);
-      }
-      const uint64_t r = enc_residue((int64_t)gld(src)[i]);
-      return sub == 0 ? csub(r + enc_residue((int64_t)gld(aux)[i]), bc.q) : r;
-    }
+    if constexpr (LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM) return finish(fetch(src, i));
     const uint64_t x = gld(src)[i];
-    if constexpr (LD == NTT_LOAD_MULM) return mont_mul(x, gld(aux)[i], bc);
     if constexpr (LD == NTT_LOAD_DOTM) return x + mont_mul(gld(aux)[i], gld(key)[i], bc);
     if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
     if constexpr (LD == NTT_LOAD_REDUCE) return x < rc.q ? x : mulmod_barrett(x, 1, rc.b);
