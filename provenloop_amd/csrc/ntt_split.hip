@@ -273,13 +273,13 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
 #pragma unroll
       for (int k = 0; k < 16; ++k) v[k] = so.load_aux(jbase + g(k));
     }
-    fwd_stages<LOGN, CB - 4, CB - 1, CB - 4>(x, jbase + p1(0), tw, ar);
+    fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, (SOp::NAUX > 0)>(x, jbase + p1(0), tw, ar);
     wave_exchange(x, lds, p1, p2);
     if constexpr (SOp::NAUX > 0) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
     }
-    fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
+    fwd_stages<LOGN, 0, CB - 5, 0, A, (SOp::NAUX > 0)>(x, jbase + p2(0), tw, ar);
     wave_exchange(x, lds, p2, g);
 #pragma unroll
     for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so.apply_prep(ar, x[k], c[NP > 1 ? k : 0]);
