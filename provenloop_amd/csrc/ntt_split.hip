@@ -61,7 +61,7 @@ __device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
 // BATCH, each stage's twiddles (16 >> (rb + 1) of them) are all requested
 // before its first butterfly, for kernels whose register pressure otherwise
 // leads the scheduler to wait on each twiddle in turn.
-template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = false>
+template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = true>
 __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar) {
 #pragma unroll
@@ -92,19 +92,33 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, G
 }
 
 // Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
-template <int LOGN, int EB, int BLO, int BHI, class A>
+// With BATCH, as in fwd_stages, each stage's twiddles are requested before
+// its first butterfly.
+template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH = true>
 __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar, const LimbConst& lc) {
 #pragma unroll
   for (int b = BLO; b <= BHI; ++b) {
     const int rb = b - EB;
     const uint32_t base = ((1u << LOGN) | f) >> (b + 1);
+    if (b == LOGN - 1) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (k & (1 << rb)) continue;
-      if (b == LOGN - 1) {
-        ar.inv_last(x[k], x[k | (1 << rb)], lc);
-      } else {
+      for (int k = 0; k < 16; ++k)
+        if (!(k & (1 << rb))) ar.inv_last(x[k], x[k | (1 << rb)], lc);
+    } else if constexpr (BATCH) {
+      constexpr int NT = 16 >> 1;
+      typename A::Tw t[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        if (j < (16 >> (rb + 1))) t[j] = ld16(tw, base | (uint32_t)j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (!(k & (1 << rb))) ar.inv(x[k], x[k | (1 << rb)], t[k >> (rb + 1)]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k & (1 << rb)) continue;
         const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
         ar.inv(x[k], x[k | (1 << rb)], t);
       }
