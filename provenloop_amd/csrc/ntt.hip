@@ -136,15 +136,23 @@ __device__ __forceinline__ void inv_pass(typename A::V (&x)[Shape<LOGN>::E], uin
   for (int b = BLO; b <= BHI; ++b) {
     const int rb = b - LO;
     const uint32_t base = ((uint32_t)S::N | jhi) >> (b + 1);
+    if (b == LOGN - 1) {
 #pragma unroll
-    for (int k = 0; k < S::E; ++k) {
-      if (k & (1 << rb)) continue;
-      const int k2 = k | (1 << rb);
-      if (b == LOGN - 1) {
-        ar.inv_last(x[k], x[k2], lc);
-      } else {
-        ar.inv(x[k], x[k2], ld16(tw, base | (uint32_t)(k >> (rb + 1))));
-      }
+      for (int k = 0; k < S::E; ++k)
+        if (!(k & (1 << rb))) ar.inv_last(x[k], x[k | (1 << rb)], lc);
+    } else {
+      // the stage's twiddles (E >> (rb + 1) of them) requested before its
+      // first butterfly, so they arrive together (measured faster here; in
+      // the forward passes the compiler's own schedule was faster)
+      constexpr int NT = S::E >> 1;
+      typename A::Tw t[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        if (j < (S::E >> (rb + 1))) t[j] = ld16(tw, base | (uint32_t)j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < S::E; ++k)
+        if (!(k & (1 << rb))) ar.inv(x[k], x[k | (1 << rb)], t[k >> (rb + 1)]);
     }
   }
   if (BHI != LOGN - 1) {
