@@ -471,8 +471,12 @@ def run_saturation(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 100 tokens; 20 steps for the saturation workload)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 200 tokens, about 90 ms: the synchronised "
+                         "per-token time settles over the first ~200 tokens; 3 steps for the saturation "
+                         "workload)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ntt-only", action="store_true",
@@ -487,6 +491,10 @@ def main():
                     help="token: the per-token Qwen2.5-1.5B pass (the reported line); moe: its CryptoMOE "
                          "variant; saturation: 32 sessions at Qwen2.5-7B shape on N=32768 with 8 limbs")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 20 if args.workload == "saturation" else 100
+    if args.warmup is None:
+        args.warmup = 3 if args.workload == "saturation" else 200
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by session/token "
               "with no cross-GPU exchange, so N GPUs scale the one-GPU figure)", file=sys.stderr)
