@@ -32,7 +32,6 @@ import ctypes as C
 import json
 import os
 import sys
-import threading
 import time
 
 import numpy as np
@@ -209,41 +208,89 @@ class CpuLayer:
         return out, cts, ct
 
 
-def cpu_baseline(cpu, budget_s=8.0, threads=None):
-    """Deltas/s of the oracle on this host: 1 thread, then `threads` threads."""
+def cpu_share():
+    """Cores this process may run on: the host's count, the affinity mask and the
+    cgroup CPU quota (a one-GPU job gets a share of the host), and the share."""
+    host = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = host
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    share = aff if quota is None else max(1, min(aff, int(quota)))
+    return {"host_cores": host, "affinity_cores": aff, "cgroup_quota_cores": quota, "share": share}
+
+
+def _cpu_worker(w, workers, ready, go, stop_at, out):
+    """One CPU-baseline process: its own oracle context and plaintexts, then
+    layers w, w + workers, ... of token 0 until stop_at (time.time())."""
+    A, B = make_workload()
+    cpu = CpuLayer(A, B)
+    hs, seeds = hidden_states(0), seeds_for(0)
+    ready.put(w)
+    go.wait()
+    k = w
+    done = 0
+    while time.time() < stop_at.value:
+        cpu.run(k % LAYERS, hs[k % LAYERS], seeds[k % LAYERS])
+        done += 1
+        k += workers
+    out.put(done)
+
+
+def cpu_baseline(cpu, budget_s=12.0):
+    """Deltas/s of the oracle on this host: one thread in this process, then one
+    process per core of the CPU share (each its own oracle context; the
+    reference core is single-threaded per operation, so the layers run side
+    by side)."""
+    import multiprocessing as mp
+
     hs = hidden_states(0)
     seeds = seeds_for(0)
-
-    def one(l):
-        cpu.run(l % LAYERS, hs[l % LAYERS], seeds[l % LAYERS])
-
     t0 = time.perf_counter()
     n1 = 0
-    while time.perf_counter() - t0 < budget_s / 2 or n1 == 0:
-        one(n1)
+    while time.perf_counter() - t0 < budget_s / 3 or n1 == 0:
+        cpu.run(n1 % LAYERS, hs[n1 % LAYERS], seeds[n1 % LAYERS])
         n1 += 1
     single = 2 * n1 / (time.perf_counter() - t0)
-    threads = threads or max(1, min(16, os.cpu_count() or 1))
-    count = [0]
-    lock = threading.Lock()
-    stop = time.perf_counter() + budget_s / 2
+    share = cpu_share()
+    workers = share["share"]
+    ctx = mp.get_context("spawn")  # fresh interpreters: no GPU runtime is inherited
+    ready, out, go = ctx.Queue(), ctx.Queue(), ctx.Event()
+    stop_at = ctx.Value("d", 0.0)
+    procs = [ctx.Process(target=_cpu_worker, args=(w, workers, ready, go, stop_at, out)) for w in range(workers)]
+    def collect(q, what, limit):
+        got, deadline = [], time.time() + limit
+        while len(got) < len(procs):
+            try:
+                got.append(q.get(timeout=1.0))
+            except Exception:  # queue.Empty: check that every worker is still alive
+                dead = [p.exitcode for p in procs if p.exitcode not in (None, 0)]
+                if dead or time.time() > deadline:
+                    for p in procs:
+                        p.kill()
+                    raise RuntimeError(f"CPU baseline workers failed while {what} (exit codes {dead})")
+        return got
 
-    def worker(w):
-        k = w
-        while time.perf_counter() < stop:
-            one(k)
-            with lock:
-                count[0] += 1
-            k += threads
-
-    t1 = time.perf_counter()
-    ws = [threading.Thread(target=worker, args=(w,)) for w in range(threads)]
-    for w in ws:
-        w.start()
-    for w in ws:
-        w.join()
-    multi = 2 * count[0] / (time.perf_counter() - t1)
-    return single, multi, threads, n1, count[0]
+    for p in procs:
+        p.start()
+    collect(ready, "setting up", 600)
+    span = 2 * budget_s / 3
+    start = time.time()
+    stop_at.value = start + span
+    go.set()
+    total = sum(collect(out, "running", 600 + span))
+    elapsed = time.time() - start
+    for p in procs:
+        p.join(timeout=60)
+    multi = 2 * total / elapsed
+    return single, multi, workers, n1, total, share
 
 
 def cpu_model():
@@ -578,8 +625,9 @@ def main():
     if args.no_cpu:
         cpu_single = cpu_multi = None
         threads = n1 = nm = 0
+        share = cpu_share()
     else:
-        cpu_single, cpu_multi, threads, n1, nm = cpu_baseline(cpu, args.cpu_budget)
+        cpu_single, cpu_multi, threads, n1, nm, share = cpu_baseline(cpu, args.cpu_budget)
 
     line = {
         "metric": METRIC,
@@ -640,9 +688,13 @@ def main():
             "cores": threads,
             "kind": "port",
             "sample": f"CPU oracle, one layer (encrypt_pk + 2 projections x 4 x (ct x pt, rescale, decrypt)) "
-                      f"repeated: {n1} layers on 1 thread, {nm} layers on {threads} threads; "
-                      f"single-thread {cpu_single:.3f} deltas/s; host {cpu_model()}",
+                      f"of token 0 repeated: {n1} layers on 1 thread, then {nm} layers in {threads} processes "
+                      f"(one per core of this job's CPU share) over {2 * args.cpu_budget / 3:.0f} s",
             "single_thread_value": round(cpu_single, 3),
+            "host_cores": share["host_cores"],
+            "affinity_cores": share["affinity_cores"],
+            "cgroup_quota_cores": share["cgroup_quota_cores"],
+            "cpu_model": cpu_model(),
             "gpu_over_cpu": round(value / cpu_multi, 1),
         },
     }

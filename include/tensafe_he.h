@@ -12,9 +12,14 @@
  *  - All functions return 0 on success and a negative TH_E* code on error;
  *    th_last_error() returns a thread-local message for the last failure.
  *    No C++ exception or panic crosses this boundary.
- *  - Handles (th_ctx, th_sk, th_pk, th_ct, th_pt) are opaque and owned by the
- *    library; release them with the matching *_free. Ciphertext, key and
- *    plaintext data stay resident in device memory (HBM) for their lifetime.
+ *  - Handles (th_ctx, th_sk, th_pk, th_ct, th_pt, th_lora) are opaque and
+ *    owned by the library; release them with the matching *_free. Ciphertext,
+ *    key and plaintext data stay resident in device memory (HBM) for their
+ *    lifetime. Keys, ciphertexts, plaintexts and LoRA sets hold a reference
+ *    to their context, so they may be freed before or after it (as the
+ *    reference's objects outlive its CkksContext): th_ctx_free refuses new
+ *    work on the context (TH_ESTATE) and its device memory is released when
+ *    the last handle made from it is freed.
  *  - Host input arrays are caller-owned and only read during the call; host
  *    output arrays are caller-owned and fully written before return.
  *  - `has_seed == 0` draws the seed from the OS (the reference's
@@ -77,15 +82,30 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
 /* Context options (no counterpart in the reference; defaults shown first).
  * TH_OPT_SAMPLER: where seeded encrypt_pk draws (u, e0, e1):
  *   TH_SAMPLER_DEVICE (default) - ChaCha20 + Box-Muller on the GPU, same
- *     stream positions as the reference; the Gaussian uses the device's
- *     log/cos, so a sample could differ from glibc's only if the two straddle
- *     a rounding boundary (never observed; see the sampler tests);
+ *     stream positions as the reference; draws whose rounding could depend on
+ *     the math library are redrawn on the host (TH_OPT_SAMPLER_BAND);
  *   TH_SAMPLER_HOST - the host draws them exactly as the reference does.
  * TH_OPT_FORCE_SERIAL_SAMPLER: 1 makes the device sampler replay every
- *   stream serially (the path taken after a range_u32 rejection); testing only. */
-enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2 };
+ *   stream serially (the path taken after a range_u32 rejection); testing only.
+ * TH_OPT_SAMPLER_BAND: v in [-52, -1], default -36: the device sampler flags
+ *   every Gaussian draw whose z * 3.19 lies within 2^v of a rounding boundary
+ *   k + 1/2 (where the device's log/cos could round differently from glibc's;
+ *   their difference stays below about 2^-45), and such an input's randomness
+ *   is drawn again on the host with glibc, so the device sampler's draws equal
+ *   the reference's in every case. Calls that return results check the flags
+ *   before returning (th_encrypt_pk and th_encrypt_pk_batch therefore wait for
+ *   their work); tokens th_lora_deltas queues without waiting are checked at
+ *   the next th_ctx_sync, th_memcpy_d2h, th_lora_free or synchronising call,
+ *   which queues a flagged token again (and, in order, the tokens queued after
+ *   it) before returning. A wider band only makes the host redraw more often
+ *   (tests use it to exercise that path). */
+enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2, TH_OPT_SAMPLER_BAND = 3 };
 enum { TH_SAMPLER_DEVICE = 0, TH_SAMPLER_HOST = 1 };
 int th_ctx_set_option(th_ctx* ctx, int option, int64_t value);
+/* Counters of the context (no counterpart in the reference): the number of
+ * encrypt_pk inputs whose randomness the device sampler flagged and the host
+ * drew again with glibc (TH_OPT_SAMPLER_BAND). */
+int th_ctx_stats(th_ctx* ctx, uint64_t* redrawn_inputs);
 
 /* ---------------------------------------------------------------- keys */
 /* Replaces CkksContext.keygen (lib.rs:91-99, ciphertext.rs:77-103). */
@@ -139,7 +159,9 @@ int th_ct_pt_mul_ntt(th_ctx* ctx, const th_ct* ct, const th_pt* pt, th_ct** out)
  * (the ZeRo-MOAI column-packed matvec batches, inference_engine.py:1292-1316). */
 int th_ct_pt_mul_ntt_batch(th_ctx* ctx, const th_ct* const* cts, const th_pt* const* pts, size_t count,
                            th_ct** outs);
-/* Replace CkksContext.ct_add / ct_sub (lib.rs:198-215, ciphertext.rs:435-466). */
+/* Replace CkksContext.ct_add / ct_sub (lib.rs:198-215, ciphertext.rs:435-466).
+ * The result has a's limbs and scale; b must have at least as many limbs
+ * (RnsPoly::add/sub run over self's limbs, rns.rs:217-240). */
 int th_ct_add(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out);
 int th_ct_sub(th_ctx* ctx, const th_ct* a, const th_ct* b, th_ct** out);
 /* Replaces CkksContext.rescale (lib.rs:218-225, ciphertext.rs:476-535). */
@@ -226,7 +248,13 @@ int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, ui
  *   inter:  NULL, or a host array of n_batches x cols segment sums.
  * With hidden and deltas in device memory and inter == NULL the call only
  * queues the token's kernels on the context stream and returns (no host
- * synchronisation; order later work with th_ctx_stream / th_ctx_sync).
+ * synchronisation; order later work with th_ctx_stream / th_ctx_sync). The
+ * device input, the output buffer and the keys must then stay valid until the
+ * next th_ctx_sync (or th_memcpy_d2h): if a Gaussian draw of the token landed
+ * in the sampler's band (TH_OPT_SAMPLER_BAND) that call queues the token again
+ * from glibc draws. Work the caller orders after the token on the stream sees
+ * its first result; read the deltas after th_ctx_sync to have them exact in
+ * every case.
  * Otherwise it returns after one synchronisation of the stream and one
  * device-to-host copy. */
 int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
@@ -257,7 +285,8 @@ int th_pk_import(th_ctx* ctx, const uint8_t* buf, size_t len, th_pk** out);
  * device pointer (on_device == 1; asynchronous on the context stream). */
 int th_ntt_forward_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device);
 int th_ntt_inverse_batch(th_ctx* ctx, uint64_t* polys, size_t count, uint32_t limbs, int on_device);
-/* Device-memory helpers for callers without their own allocator. */
+/* Device-memory helpers for callers without their own allocator. th_dev_free
+ * accepts only a pointer from th_dev_alloc that has not been freed yet. */
 int th_dev_alloc(th_ctx* ctx, size_t bytes, void** out);
 int th_dev_free(th_ctx* ctx, void* p);
 int th_memcpy_h2d(th_ctx* ctx, void* dst, const void* src, size_t bytes);

@@ -227,6 +227,8 @@ RnsPoly RnsPoly::zero(size_t n, size_t num_limbs) {
 // rns.rs:217-227
 RnsPoly RnsPoly::add(const RnsPoly& o, const std::vector<Modulus>& moduli) const {
   if (n != o.n) throw std::invalid_argument("RnsPoly::add size mismatch");
+  // o.limbs[l] for every l of self: Rust panics (index out of bounds) when o has fewer limbs
+  if (o.limbs.size() < limbs.size()) throw std::invalid_argument("RnsPoly::add: index out of bounds");
   RnsPoly r = zero(n, limbs.size());
   for (size_t l = 0; l < limbs.size(); ++l) {
     uint64_t q = moduli[l].value;
@@ -238,6 +240,8 @@ RnsPoly RnsPoly::add(const RnsPoly& o, const std::vector<Modulus>& moduli) const
 // rns.rs:230-240
 RnsPoly RnsPoly::sub(const RnsPoly& o, const std::vector<Modulus>& moduli) const {
   if (n != o.n) throw std::invalid_argument("RnsPoly::sub size mismatch");
+  // o.limbs[l] for every l of self: Rust panics (index out of bounds) when o has fewer limbs
+  if (o.limbs.size() < limbs.size()) throw std::invalid_argument("RnsPoly::sub: index out of bounds");
   RnsPoly r = zero(n, limbs.size());
   for (size_t l = 0; l < limbs.size(); ++l) {
     uint64_t q = moduli[l].value;
@@ -249,6 +253,8 @@ RnsPoly RnsPoly::sub(const RnsPoly& o, const std::vector<Modulus>& moduli) const
 // rns.rs:243-253 — iterates over self's limbs (other may have more limbs).
 RnsPoly RnsPoly::hadamard_mul(const RnsPoly& o, const std::vector<Modulus>& moduli) const {
   if (n != o.n) throw std::invalid_argument("RnsPoly::hadamard_mul size mismatch");
+  // o.limbs[l] for every l of self: Rust panics (index out of bounds) when o has fewer limbs
+  if (o.limbs.size() < limbs.size()) throw std::invalid_argument("RnsPoly::hadamard_mul: index out of bounds");
   RnsPoly r = zero(n, limbs.size());
   for (size_t l = 0; l < limbs.size(); ++l) {
     const Modulus& m = moduli[l];

@@ -1,6 +1,7 @@
 // Flat C interface of the CPU oracle, for ctypes (oracle/oracle.py).
 // Test infrastructure only (see oracle.h): called by tests/, the smoke check
 // and bench.py's CPU-baseline leg, never by the product path.
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -305,6 +306,32 @@ int orc_encrypt(void* c, const double* z, size_t len, void* sk, uint64_t seed, v
     *out = new Ciphertext(((CkksContext*)c)->encrypt(z, len, *(SecretKey*)sk, r));
   });
 }
+// tensafe-he-python/src/lib.rs:230-258 (batch_encrypt): ONE TenSafeRng for the
+// whole batch; input i (z + i*stride, lens[i] values) is zero-padded or
+// truncated to the slot count (:251-253) and encrypted with ctx.encrypt in
+// order, so each encryption continues the stream where the previous stopped.
+int orc_batch_encrypt(void* c, const double* z, const size_t* lens, size_t stride, size_t count, void* sk,
+                      uint64_t seed, void** outs) {
+  return guard([&] {
+    CkksContext* ctx = (CkksContext*)c;
+    const size_t slots = ctx->params.poly_degree / 2;
+    TenSafeRng r = TenSafeRng::from_seed(seed);
+    std::vector<Ciphertext*> made;
+    try {
+      for (size_t i = 0; i < count; ++i) {
+        std::vector<double> padded(slots, 0.0);
+        const size_t n = std::min(lens[i], slots);
+        std::copy(z + i * stride, z + i * stride + n, padded.begin());
+        made.push_back(new Ciphertext(ctx->encrypt(padded.data(), slots, *(SecretKey*)sk, r)));
+      }
+    } catch (...) {
+      for (Ciphertext* x : made) delete x;
+      throw;
+    }
+    for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+  });
+}
+
 int orc_encrypt_pk(void* c, const double* z, size_t len, void* pk, uint64_t seed, void** out) {
   return guard([&] {
     TenSafeRng r = TenSafeRng::from_seed(seed);

@@ -92,6 +92,7 @@ def lib():
         "orc_pk_data": (C.c_int, [VP, u64p, u64p]),
         "orc_encrypt": (C.c_int, [VP, f64p, SZ, VP, U64, C.POINTER(VP)]),
         "orc_encrypt_pk": (C.c_int, [VP, f64p, SZ, VP, U64, C.POINTER(VP)]),
+        "orc_batch_encrypt": (C.c_int, [VP, f64p, VP, SZ, SZ, VP, U64, VP]),
         "orc_encrypt_pk_with": (C.c_int, [VP, f64p, SZ, VP, u8p, i64p, i64p, C.POINTER(VP)]),
         "orc_ct_info": (C.c_int, [VP, C.POINTER(SZ), C.POINTER(C.c_double)]),
         "orc_ct_data": (C.c_int, [VP, u64p, u64p]),
@@ -430,6 +431,21 @@ class Context:
     def encrypt(self, z, sk, seed):
         z = _f64(z)
         return self._new(Ciphertext, lib().orc_encrypt, self.ptr, z, z.size, sk.ptr, seed)
+
+    def batch_encrypt(self, arrays, sk, seed):
+        """lib.rs:230-258: one seeded stream shared by every encryption, in order."""
+        arrays = [_f64(a) for a in arrays]
+        if not arrays:
+            return []
+        width = max(a.size for a in arrays)
+        flat = np.zeros((len(arrays), max(width, 1)), np.float64)
+        for i, a in enumerate(arrays):
+            flat[i, : a.size] = a
+        lens = np.array([a.size for a in arrays], np.uint64)
+        outs = (VP * len(arrays))()
+        _check(lib().orc_batch_encrypt(self.ptr, flat.reshape(-1), lens.ctypes.data, flat.shape[1],
+                                       len(arrays), sk.ptr, seed, outs))
+        return [Ciphertext(outs[i]) for i in range(len(arrays))]
 
     def encrypt_pk(self, z, pk, seed):
         z = _f64(z)

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, "libtensafe_he_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "tensafe_he.h")
 
 TH_OK, TH_EINVAL, TH_EDEVICE, TH_ENOMEM, TH_ESTATE = 0, -1, -2, -3, -4
-TH_OPT_SAMPLER, TH_OPT_FORCE_SERIAL_SAMPLER = 1, 2
+TH_OPT_SAMPLER, TH_OPT_FORCE_SERIAL_SAMPLER, TH_OPT_SAMPLER_BAND = 1, 2, 3
 TH_SAMPLER_DEVICE, TH_SAMPLER_HOST = 0, 1
 
 VP = C.c_void_p
@@ -38,6 +38,7 @@ _SIGS = {
     "th_ctx_sync": (I32, [VP]),
     "th_ctx_stream": (I32, [VP, PVP]),
     "th_ctx_set_option": (I32, [VP, I32, C.c_int64]),
+    "th_ctx_stats": (I32, [VP, C.POINTER(U64)]),
     "th_keygen": (I32, [VP, U64, I32, PVP]),
     "th_keygen_public": (I32, [VP, VP, U64, I32, PVP]),
     "th_sk_free": (I32, [VP]),

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
                                                               const double* __restrict__ stage_im, uint32_t logn,
                                                               const double* __restrict__ z_base,
                                                               const SampleJob* __restrict__ fix, SeedBlock sb,
-                                                              int use_sb, int force_serial) {
+                                                              int use_sb, int force_serial, BandArgs band) {
   extern __shared__ double sh[];
   const uint32_t n = 1u << logn, S = n / 2;
   const uint32_t M = n >> LP;
@@ -122,7 +122,8 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   // the sampler launch queued before this one left its rejection check here
   if (fix && part == 0 && threadIdx.x == 0) {
     const SampleJob sj = fix[blockIdx.y];
-    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial);
+    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial,
+                   band.flags ? band.flags + blockIdx.y : nullptr, band.band);
   }
 }
 
@@ -214,7 +215,7 @@ size_t encode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base, const SampleJob* fix, const uint64_t* seeds,
-                         int force_serial) {
+                         int force_serial, BandArgs band) {
   if (!njobs) return hipSuccess;
   if (fix && njobs > SEEDS_PER_LAUNCH) return hipErrorInvalidValue;
   SeedBlock sb{};
@@ -238,7 +239,7 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
     e = allow_full_lds<k_encode_parts<LP>>();                                                              \
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
-                       stage_im, logn, z_base, fix, sb, (int)(seeds != nullptr), force_serial);            \
+                       stage_im, logn, z_base, fix, sb, (int)(seeds != nullptr), force_serial, band);     \
     hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im, \
                        stage_re, stage_im, logn, L);                                                       \
     return hipGetLastError();

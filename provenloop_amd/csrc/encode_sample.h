@@ -21,6 +21,19 @@ struct SampleJob;
 // Seeds travel with a sampler launch for up to this many jobs.
 constexpr uint32_t SEEDS_PER_LAUNCH = 64;
 
+// Band flags of a sampler launch: flags[j] (one byte per job, in host-visible
+// memory; null for none) is set to 1 when a Gaussian draw of job j lands
+// within `band` of a rounding boundary (near_rounding_boundary), where the
+// device's log/cos could round differently from glibc's. The host then
+// redraws that job's randomness with glibc.
+struct BandArgs {
+  uint8_t* flags;
+  double band;
+};
+// Default band: 2^-36, about 2^9 times the largest difference between the
+// device's and glibc's z * 3.19.
+constexpr double SAMPLER_BAND_DEFAULT = 0x1p-36;
+
 // Encode z and write the per-limb residues of m (+ e0), e1 and u. With
 // z_base, job i reads its input at z_base + i * (rep_d, or N/2 without
 // replication) instead of its z field. With fix (the sample jobs of a
@@ -30,7 +43,7 @@ constexpr uint32_t SEEDS_PER_LAUNCH = 64;
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base = nullptr, const SampleJob* fix = nullptr,
-                         const uint64_t* seeds = nullptr, int force_serial = 0);
+                         const uint64_t* seeds = nullptr, int force_serial = 0, BandArgs band = BandArgs{nullptr, 0.0});
 size_t encode_parts_doubles(uint32_t logn);
 
 struct SampleJob {
@@ -47,8 +60,9 @@ struct SampleJob {
 // seeds (host array, one per job) the jobs' seed fields are ignored and the
 // seeds travel in the launch arguments. Jobs with a reject flag (all or none
 // of them) skip the re-derivation pass: the block kernel raises the flag and
-// only flagged jobs are replayed; the flag is cleared again.
+// only flagged jobs are replayed; the flag is cleared again. band: the band
+// flags of the njobs jobs (BandArgs).
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
-                            const uint64_t* seeds = nullptr, bool flagged = false, bool fix_later = false);
+                            const uint64_t* seeds, bool flagged, bool fix_later, BandArgs band);
 
 }  // namespace th

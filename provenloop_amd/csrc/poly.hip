@@ -33,11 +33,12 @@ __global__ void k_ct_pt_mul(const CtPtJob* __restrict__ jobs, const BarrettConst
 // out = a +/- b over 2 * limbs limb-polynomials (ciphertext.rs:435-466).
 __global__ void k_ct_addsub(const AddJob* __restrict__ jobs, const uint64_t* __restrict__ q, uint32_t n) {
   const AddJob jb = jobs[blockIdx.y];
-  const uint32_t total = 2 * jb.limbs * n;
+  const uint32_t half = jb.limbs * n, total = 2 * half;
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-    const uint32_t l = (e / n) % jb.limbs;
-    const uint64_t m = q[l];
-    const uint64_t a = gld(jb.a)[e], b = gld(jb.b)[e];
+    const bool c1 = e >= half;
+    const uint32_t r = c1 ? e - half : e;
+    const uint64_t m = q[r / n];
+    const uint64_t a = gld(c1 ? jb.a1 : jb.a0)[r], b = gld(c1 ? jb.b1 : jb.b0)[r];
     gst(jb.out)[e] = jb.sub ? submod(a, b, m) : addmod(a, b, m);
   }
 }

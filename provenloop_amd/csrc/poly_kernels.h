@@ -13,10 +13,14 @@ struct CtPtJob {
   uint32_t pad_;
 };
 
+// out = a +- b on a's limbs; the operands' c0 and c1 are addressed apart so
+// that b may hold more limbs than a.
 struct AddJob {
-  const uint64_t* a;
-  const uint64_t* b;
-  uint64_t* out;
+  const uint64_t* a0;
+  const uint64_t* a1;
+  const uint64_t* b0;
+  const uint64_t* b1;
+  uint64_t* out;  // [c0 | c1], limbs each
   uint32_t limbs;
   uint32_t sub;
 };

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <map>
 #include <mutex>
@@ -20,6 +21,7 @@
 #include <string>
 #include <thread>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "encode_sample.h"
@@ -54,11 +56,7 @@ class DevicePool {
     bytes = (bytes + 255) & ~(size_t)255;
     std::lock_guard<std::mutex> lk(mu_);
     auto& fl = free_[bytes];
-    if (!fl.empty()) {
-      void* p = fl.back();
-      fl.pop_back();
-      return p;
-    }
+    if (!fl.empty()) return take(fl);
     void* p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess || !p) {
       (void)hipGetLastError();
@@ -67,28 +65,38 @@ class DevicePool {
     sizes_[p] = bytes;
     return p;
   }
-  void put(void* p) {
-    if (!p) return;
+  // Returns a buffer to its free list; false (and nothing changes) for a
+  // pointer the pool did not hand out or one that is already free, so a
+  // second put can never make two later get() calls share one buffer.
+  bool put(void* p) {
+    if (!p) return true;
     std::lock_guard<std::mutex> lk(mu_);
     auto it = sizes_.find(p);
-    if (it == sizes_.end()) return;
+    if (it == sizes_.end() || !is_free_.insert(p).second) return false;
     free_[it->second].push_back(p);
-  }
-  bool owns(void* p) {
-    std::lock_guard<std::mutex> lk(mu_);
-    return sizes_.count(p) != 0;
+    return true;
   }
   void release_all() {
     std::lock_guard<std::mutex> lk(mu_);
     for (auto& kv : sizes_) (void)hipFree(kv.first);
     sizes_.clear();
     free_.clear();
+    is_free_.clear();
   }
 
  private:
+  // get() takes a pointer off a free list, so it is no longer free
+  void* take(std::vector<void*>& fl) {
+    void* p = fl.back();
+    fl.pop_back();
+    is_free_.erase(p);
+    return p;
+  }
+
   std::mutex mu_;
   std::unordered_map<size_t, std::vector<void*>> free_;
   std::unordered_map<void*, size_t> sizes_;
+  std::unordered_set<void*> is_free_;
 };
 
 // Pinned host staging for host<->device copies. Allocation is a bump pointer;
@@ -153,7 +161,30 @@ void parallel_for(size_t count, F&& f) {
 }  // namespace
 
 // ---------------------------------------------------------------- handles
+struct th_lora;
+struct th_pk;
+struct th_sk;
+
+// A token of th_lora_deltas queued without a host synchronisation: what it
+// takes to queue it again if one of its Gaussian draws turns out to lie in
+// the sampler's band (the redo draws that token's randomness with glibc).
+struct AsyncToken {
+  th_lora* set;
+  const th_pk* pk;
+  const th_sk* sk;
+  const double* hidden;  // device
+  std::vector<uint64_t> seeds;
+  int do_rescale;
+  double* deltas;        // device
+  uint32_t flag_off;     // band flags of its inputs
+};
+
 struct th_ctx {
+  // Lifetime: the context and every handle made from it hold one reference;
+  // th_ctx_free drops the context's own and marks it closed (no new work),
+  // and the last release frees the device memory, the stream and the object.
+  std::atomic<uint32_t> refs{1};
+  std::atomic<bool> closed{false};
   int device = 0;
   hipStream_t stream = nullptr;
   uint32_t N = 0, logn = 0, L = 0;
@@ -169,6 +200,17 @@ struct th_ctx {
   Encoder enc;
   int host_sampler = 0;   // TH_OPT_SAMPLER
   int force_serial = 0;   // TH_OPT_FORCE_SERIAL_SAMPLER
+  double band = SAMPLER_BAND_DEFAULT;  // TH_OPT_SAMPLER_BAND
+  // Band flags of the device sampler (BandArgs): pinned host bytes the
+  // kernels write through bflag_dev. A call takes a region of one byte per
+  // sampled input (take_flags); asynchronous tokens keep theirs until the
+  // next resolve_pending.
+  uint8_t* bflag_host = nullptr;
+  uint8_t* bflag_dev = nullptr;
+  uint32_t bflag_cap = 0, bflag_used = 0;
+  std::vector<AsyncToken> pending;
+  uint64_t redrawn_inputs = 0;  // inputs whose randomness was drawn again on the host (th_ctx_stats)
+  std::unordered_set<void*> user_allocs;  // th_dev_alloc buffers not yet freed
   DevicePool pool;
   StagingRing ring;
   std::map<std::pair<uint32_t, uint32_t>, double*> seg_w;  // segment-sum weights by (d, cols)
@@ -299,10 +341,67 @@ void use_device(th_ctx* c) { HIPCHK(hipSetDevice(c->device)); }
 
 size_t poly_bytes(const th_ctx* c) { return (size_t)c->N * 8; }
 
+// ---------------------------------------------------------------- handle lifetime
+void destroy_ctx(th_ctx* c);
+
+void ctx_retain(th_ctx* c) { c->refs.fetch_add(1, std::memory_order_relaxed); }
+
+// Drops one reference; the last one destroys the context.
+void ctx_release(th_ctx* c) {
+  if (c->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) destroy_ctx(c);
+}
+
+// A new handle holds a reference to its context.
+template <class H>
+H* adopt(H* h) {
+  ctx_retain(h->ctx);
+  return h;
+}
+
+void drop(th_ct* x) {
+  th_ctx* c = x->ctx;
+  c->pool.put(x->d);
+  delete x;
+  ctx_release(c);
+}
+void drop(th_pt* x) {
+  th_ctx* c = x->ctx;
+  c->pool.put(x->d);
+  delete x;
+  ctx_release(c);
+}
+void drop(th_sk* x) {
+  th_ctx* c = x->ctx;
+  if (x->dm) c->pool.put(x->dm);
+  c->pool.put(x->d);
+  delete x;
+  ctx_release(c);
+}
+void drop(th_pk* x) {
+  th_ctx* c = x->ctx;
+  if (x->dp) c->pool.put(x->dp);
+  c->pool.put(x->d);
+  delete x;
+  ctx_release(c);
+}
+
 th_ct* new_ct(th_ctx* c, uint32_t limbs, double scale) {
-  th_ct* ct = new th_ct{c, limbs, scale, nullptr};
-  ct->d = (uint64_t*)c->pool.get(2 * limbs * poly_bytes(c));
+  th_ct* ct = adopt(new th_ct{c, limbs, scale, nullptr});
+  try {
+    ct->d = (uint64_t*)c->pool.get(2 * limbs * poly_bytes(c));
+  } catch (...) {
+    drop(ct);
+    throw;
+  }
   return ct;
+}
+
+// Drops every handle of a partly built batch of outputs, then rethrows.
+template <class H>
+[[noreturn]] void drop_all_rethrow(std::vector<H*>& made) {
+  for (H* h : made) drop(h);
+  made.clear();
+  throw;
 }
 
 // Wait until everything queued on the context's stream, by this library or
@@ -314,6 +413,50 @@ void wait_stream(th_ctx* c) {
   while ((e = hipStreamQuery(c->stream)) == hipErrorNotReady) __builtin_ia32_pause();
   HIPCHK(e);
 }
+
+// ---------------------------------------------------------------- sampler band flags
+// After the stream has drained: queue again, with glibc draws, every
+// asynchronous token whose band flags are set (and, in order, the tokens
+// queued after it, which may share its outputs), then wait.
+void resolve_pending(th_ctx* c);
+
+// Waits for the stream and settles the asynchronous tokens' band flags.
+void drain(th_ctx* c) {
+  wait_stream(c);
+  resolve_pending(c);
+}
+
+// Before a key goes away: settle the queued tokens that read it.
+void settle_before_free(th_ctx* c, const void* key) {
+  std::lock_guard<std::mutex> lk(c->mu);
+  for (const AsyncToken& t : c->pending)
+    if ((const void*)t.pk == key || (const void*)t.sk == key) {
+      use_device(c);
+      drain(c);
+      return;
+    }
+}
+
+// A zeroed region of n band flags (one per sampled input) for one call.
+uint32_t take_flags(th_ctx* c, uint32_t n) {
+  need(n <= c->bflag_cap, "too many sampled inputs in one call", TH_EINVAL);
+  if (c->bflag_used + n > c->bflag_cap) drain(c);  // frees every region held by queued tokens
+  const uint32_t off = c->bflag_used;
+  memset(c->bflag_host + off, 0, n);
+  c->bflag_used += n;
+  return off;
+}
+
+// The region taken last by a call that has checked its flags.
+void release_flags(th_ctx* c, uint32_t off) { c->bflag_used = off; }
+
+bool any_flag(const th_ctx* c, uint32_t off, uint32_t n) {
+  for (uint32_t i = 0; i < n; ++i)
+    if (c->bflag_host[off + i]) return true;
+  return false;
+}
+
+BandArgs band_args(const th_ctx* c, uint32_t off) { return BandArgs{c->bflag_dev + off, c->band}; }
 
 // The public key as prepared pairs, made on the context's stream the first
 // time it is needed (queued before its first reader).
@@ -504,6 +647,7 @@ void destroy_ctx(th_ctx* c) {
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
   for (auto& kv : c->seg_p) (void)hipFree(kv.second);
+  if (c->bflag_host) (void)hipHostFree(c->bflag_host);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -546,74 +690,6 @@ void queue_encode(OpScope& sc, const double* z, size_t count, const uint8_t* u, 
                        c->d_stage_im, c->logn, c->L, c->stream));
 }
 
-// encrypt_pk of `count` padded inputs zh (host, count x N/2). Randomness comes
-// from the device sampler (seeds), or from host arrays u/e0/e1 (count x N each).
-// Queue encrypt_pk of `count` inputs already on the device (z: count x N/2
-// padded slots, or count x rep_d values replicated rep_cols times) into the
-// ciphertext buffers out[i] (2 x L limb-polys each), drawing the randomness on
-// the device from seeds (host array).
-void queue_encrypt_pk(OpScope& sc, const th_pk* pk, const double* z, size_t count, const uint64_t* seeds,
-                      uint32_t rep_d, uint32_t rep_cols, uint64_t* const* out) {
-  th_ctx* c = sc.c;
-  const uint32_t N = c->N, L = c->L;
-  uint8_t* u = (uint8_t*)sc.dev(count * N);
-  int64_t* e0 = (int64_t*)sc.dev(count * N * 8);
-  int64_t* e1 = (int64_t*)sc.dev(count * N * 8);
-  std::vector<SampleJob> sj(count);
-  for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], u + i * N, e0 + i * N, e1 + i * N, nullptr};
-  HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
-  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
-  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N, rep_d, rep_cols);
-  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
-  std::vector<EncCombineJob> cj(count);
-  for (size_t i = 0; i < count; ++i) cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, out[i]};
-  HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
-}
-
-void encrypt_pk_many(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint64_t* seeds,
-                     const uint8_t* hu, const int64_t* he0, const int64_t* he1, th_ct** outs) {
-  const uint32_t N = c->N, L = c->L, S = N / 2;
-  OpScope sc(c);
-  const double* z = (const double*)sc.upload(zh, count * S * 8);
-  const uint8_t* u;
-  const int64_t *e0, *e1;
-  if (hu) {
-    u = (const uint8_t*)sc.upload(hu, count * N);
-    e0 = (const int64_t*)sc.upload(he0, count * N * 8);
-    e1 = (const int64_t*)sc.upload(he1, count * N * 8);
-  } else {
-    uint8_t* du = (uint8_t*)sc.dev(count * N);
-    int64_t* de0 = (int64_t*)sc.dev(count * N * 8);
-    int64_t* de1 = (int64_t*)sc.dev(count * N * 8);
-    std::vector<SampleJob> sj(count);
-    for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], du + i * N, de0 + i * N, de1 + i * N, nullptr};
-    HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream));
-    u = du;
-    e0 = de0;
-    e1 = de1;
-  }
-  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
-  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N);
-  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
-  std::vector<EncCombineJob> cj(count);
-  std::vector<th_ct*> made;
-  try {
-    for (size_t i = 0; i < count; ++i) {
-      th_ct* ct = new_ct(c, L, kScale);  // ciphertext.rs:314-318
-      made.push_back(ct);
-      cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, ct->d};
-    }
-    HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
-  } catch (...) {
-    for (th_ct* ct : made) {
-      c->pool.put(ct->d);
-      delete ct;
-    }
-    throw;
-  }
-  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
-}
-
 // encrypt_pk's draws on the host (ciphertext.rs:255-273): u, then e0, then e1.
 void draw_pk_randomness(uint64_t seed, int has_seed, uint32_t N, uint8_t* u, int64_t* e0, int64_t* e1) {
   ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
@@ -622,18 +698,121 @@ void draw_pk_randomness(uint64_t seed, int has_seed, uint32_t N, uint8_t* u, int
   draw_gaussian(s, N, e1);
 }
 
+// encrypt_pk's randomness of `count` seeded inputs drawn on the host with
+// glibc, exactly as the reference draws it, in device buffers u, e0, e1
+// (count x N each) of the caller's scope.
+void upload_host_draws(OpScope& sc, const uint64_t* seeds, size_t count, uint8_t* u, int64_t* e0, int64_t* e1) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N;
+  std::vector<uint8_t> hu(count * N);
+  std::vector<int64_t> he0(count * N), he1(count * N);
+  parallel_for(count, [&](size_t i) { draw_pk_randomness(seeds[i], 1, N, &hu[i * N], &he0[i * N], &he1[i * N]); });
+  HIPCHK(hipMemcpyAsync(u, sc.up(hu), hu.size(), hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(hipMemcpyAsync(e0, sc.up(he0), he0.size() * 8, hipMemcpyDeviceToDevice, c->stream));
+  HIPCHK(hipMemcpyAsync(e1, sc.up(he1), he1.size() * 8, hipMemcpyDeviceToDevice, c->stream));
+}
+
+// Queue encrypt_pk of `count` inputs already on the device (z: count x N/2
+// padded slots, or count x rep_d values replicated rep_cols times) into the
+// ciphertext buffers out[i] (2 x L limb-polys each). The randomness comes from
+// the device sampler (seeds, band flags `band`), or, with host_draw, from the
+// host (upload_host_draws).
+void queue_encrypt_pk(OpScope& sc, const th_pk* pk, const double* z, size_t count, const uint64_t* seeds,
+                      uint32_t rep_d, uint32_t rep_cols, uint64_t* const* out, bool host_draw, BandArgs band) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, L = c->L;
+  uint8_t* u = (uint8_t*)sc.dev(count * N);
+  int64_t* e0 = (int64_t*)sc.dev(count * N * 8);
+  int64_t* e1 = (int64_t*)sc.dev(count * N * 8);
+  if (host_draw) {
+    upload_host_draws(sc, seeds, count, u, e0, e1);
+  } else {
+    std::vector<SampleJob> sj(count);
+    for (size_t i = 0; i < count; ++i) sj[i] = SampleJob{seeds[i], u + i * N, e0 + i * N, e1 + i * N, nullptr};
+    HIPCHK(launch_sample_pk(sc.up(sj), (uint32_t)count, N, c->force_serial, c->stream, nullptr, false, false, band));
+  }
+  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
+  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N, rep_d, rep_cols);
+  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
+  std::vector<EncCombineJob> cj(count);
+  for (size_t i = 0; i < count; ++i) cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, out[i]};
+  HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
+}
+
+// Queue encrypt_pk of `count` padded inputs (device z, count x N/2) with
+// host-supplied randomness (host arrays, count x N each) into out[i].
+void queue_encrypt_pk_explicit(OpScope& sc, const th_pk* pk, const double* z, size_t count, const uint8_t* hu,
+                               const int64_t* he0, const int64_t* he1, uint64_t* const* out) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, L = c->L;
+  const uint8_t* u = (const uint8_t*)sc.upload(hu, count * N);
+  const int64_t* e0 = (const int64_t*)sc.upload(he0, count * N * 8);
+  const int64_t* e1 = (const int64_t*)sc.upload(he1, count * N * 8);
+  uint64_t* prep = (uint64_t*)sc.dev(count * 3 * L * poly_bytes(c));
+  queue_encode(sc, z, count, u, e0, e1, prep, (size_t)3 * L * N);
+  ntt_strided(c, false, prep, prep, (uint32_t)(count * 3 * L), L);
+  std::vector<EncCombineJob> cj(count);
+  for (size_t i = 0; i < count; ++i) cj[i] = EncCombineJob{prep + i * 3 * L * N, pk->d, pk->d + (size_t)L * N, out[i]};
+  HIPCHK(launch_encrypt_combine(sc.up(cj), (uint32_t)count, c->d_bc, N, L, c->stream));
+}
+
+// New ciphertexts for `count` encrypt_pk outputs (ciphertext.rs:314-318).
+std::vector<th_ct*> new_encrypt_outputs(th_ctx* c, size_t count) {
+  std::vector<th_ct*> made;
+  try {
+    for (size_t i = 0; i < count; ++i) made.push_back(new_ct(c, c->L, kScale));
+  } catch (...) {
+    drop_all_rethrow(made);
+  }
+  return made;
+}
+
+// encrypt_pk of `count` padded inputs zh (host, count x N/2) with
+// host-supplied randomness (count x N each).
+void encrypt_pk_explicit_many(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint8_t* hu,
+                              const int64_t* he0, const int64_t* he1, th_ct** outs) {
+  std::vector<th_ct*> made = new_encrypt_outputs(c, count);
+  try {
+    OpScope sc(c);
+    const double* z = (const double*)sc.upload(zh, count * (c->N / 2) * 8);
+    std::vector<uint64_t*> dst(count);
+    for (size_t i = 0; i < count; ++i) dst[i] = made[i]->d;
+    queue_encrypt_pk_explicit(sc, pk, z, count, hu, he0, he1, dst.data());
+  } catch (...) {
+    drop_all_rethrow(made);
+  }
+  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
+}
+
 // Seeded encrypt_pk of `count` padded inputs through the configured sampler.
+// With the device sampler the call waits for its work: if a Gaussian draw
+// landed in the band, the inputs are encrypted again from glibc draws
+// (host sampler) into the same ciphertexts before they are returned.
 void encrypt_pk_seeded(th_ctx* c, const th_pk* pk, const double* zh, size_t count, const uint64_t* seeds,
                        th_ct** outs) {
-  if (!c->host_sampler) {
-    encrypt_pk_many(c, pk, zh, count, seeds, nullptr, nullptr, nullptr, outs);
-    return;
+  const uint32_t N = c->N, S = N / 2;
+  std::vector<th_ct*> made = new_encrypt_outputs(c, count);
+  try {
+    OpScope sc(c);
+    const double* z = (const double*)sc.upload(zh, count * S * 8);
+    std::vector<uint64_t*> dst(count);
+    for (size_t i = 0; i < count; ++i) dst[i] = made[i]->d;
+    if (c->host_sampler) {
+      queue_encrypt_pk(sc, pk, z, count, seeds, 0, 0, dst.data(), true, BandArgs{nullptr, 0.0});
+    } else {
+      const uint32_t off = take_flags(c, (uint32_t)count);
+      queue_encrypt_pk(sc, pk, z, count, seeds, 0, 0, dst.data(), false, band_args(c, off));
+      wait_stream(c);
+      if (any_flag(c, off, (uint32_t)count)) {
+        queue_encrypt_pk(sc, pk, z, count, seeds, 0, 0, dst.data(), true, BandArgs{nullptr, 0.0});
+        c->redrawn_inputs += count;
+      }
+      release_flags(c, off);
+    }
+  } catch (...) {
+    drop_all_rethrow(made);
   }
-  const uint32_t N = c->N;
-  std::vector<uint8_t> u(count * N);
-  std::vector<int64_t> e0(count * N), e1(count * N);
-  parallel_for(count, [&](size_t i) { draw_pk_randomness(seeds[i], 1, N, &u[i * N], &e0[i * N], &e1[i * N]); });
-  encrypt_pk_many(c, pk, zh, count, nullptr, u.data(), e0.data(), e1.data(), outs);
+  for (size_t i = 0; i < count; ++i) outs[i] = made[i];
 }
 
 // ---------------------------------------------------------------- pipelines on raw device ciphertexts
@@ -833,11 +1012,7 @@ void rescale_many(th_ctx* c, const th_ct* const* cts, size_t count, th_ct** outs
     OpScope sc(c);
     queue_rescale(sc, views_of(cts, count), dst.data());
   } catch (...) {
-    for (th_ct* o : made) {
-      c->pool.put(o->d);
-      delete o;
-    }
-    throw;
+    drop_all_rethrow(made);
   }
   for (size_t i = 0; i < count; ++i) outs[i] = made[i];
 }
@@ -845,15 +1020,15 @@ void rescale_many(th_ctx* c, const th_ct* const* cts, size_t count, th_ct** outs
 th_pt* encode_pt(th_ctx* c, const double* z, size_t n) {
   std::vector<double> pad(c->N / 2);
   pad_input(c, z, n, pad.data());
-  th_pt* pt = new th_pt{c, c->L, (uint64_t*)c->pool.get(c->L * poly_bytes(c))};
+  th_pt* pt = adopt(new th_pt{c, c->L, nullptr});
   try {
+    pt->d = (uint64_t*)c->pool.get(c->L * poly_bytes(c));
     OpScope sc(c);
     const double* zd = sc.up(pad);
     queue_encode(sc, zd, 1, nullptr, nullptr, nullptr, pt->d, 0);
     ntt_strided(c, false, pt->d, pt->d, c->L, c->L);
   } catch (...) {
-    c->pool.put(pt->d);
-    delete pt;
+    drop(pt);
     throw;
   }
   return pt;
@@ -875,29 +1050,31 @@ void ct_pt_many(th_ctx* c, const th_ct* const* cts, const th_pt* const* pts, siz
     OpScope sc(c);
     queue_ct_pt(sc, views_of(cts, count), p.data(), dst.data());
   } catch (...) {
-    for (th_ct* o : made) {
-      c->pool.put(o->d);
-      delete o;
-    }
-    throw;
+    drop_all_rethrow(made);
   }
   for (size_t i = 0; i < count; ++i) outs[i] = made[i];
 }
 
+// ct_add / ct_sub (ciphertext.rs:435-466): the result has a's limbs and
+// scale; RnsPoly::add/sub (rns.rs:217-240) run over self's limbs and index
+// the other operand's, so b may have more limbs (a rescaled ciphertext plus
+// one at the top level) and fewer is the reference's out-of-bounds panic.
 void add_sub(th_ctx* c, const th_ct* a, const th_ct* b, bool sub, th_ct** out) {
   check_ct(c, a);
   check_ct(c, b);
   // ciphertext.rs:436-441
   need(fabs(a->scale - b->scale) < 1.0, std::string("Scale mismatch in ") + (sub ? "ct_sub" : "ct_add"));
-  need(a->limbs == b->limbs, "limb count mismatch");
+  need(b->limbs >= a->limbs, std::string(sub ? "ct_sub" : "ct_add") + ": the second ciphertext has " +
+                                 std::to_string(b->limbs) + " limbs, fewer than the first's " +
+                                 std::to_string(a->limbs));
   th_ct* o = new_ct(c, a->limbs, a->scale);
-  AddJob j{a->d, b->d, o->d, a->limbs, sub ? 1u : 0u};
+  const size_t N = c->N;
+  AddJob j{a->d, a->d + (size_t)a->limbs * N, b->d, b->d + (size_t)b->limbs * N, o->d, a->limbs, sub ? 1u : 0u};
   try {
     OpScope sc(c);
     HIPCHK(launch_ct_addsub(sc.up(std::vector<AddJob>{j}), 1, a->limbs, c->d_q, c->N, c->stream));
   } catch (...) {
-    c->pool.put(o->d);
-    delete o;
+    drop(o);
     throw;
   }
   *out = o;
@@ -980,6 +1157,9 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       build_tables(c);
       c->ring.init(64u << 20);
+      c->bflag_cap = 1u << 16;
+      HIPCHK(hipHostMalloc((void**)&c->bflag_host, c->bflag_cap, hipHostMallocMapped | hipHostMallocCoherent));
+      HIPCHK(hipHostGetDevicePointer((void**)&c->bflag_dev, c->bflag_host, 0));
     } catch (...) {
       destroy_ctx(c);
       throw;
@@ -989,7 +1169,17 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
 }
 
 int th_ctx_free(th_ctx* ctx) {
-  return guarded([&] { destroy_ctx(ctx); });
+  return guarded([&] {
+    if (!ctx) return;
+    need(!ctx->closed.exchange(true), "context already freed", TH_ESTATE);
+    {
+      // settle queued tokens while their handles are certainly alive
+      std::lock_guard<std::mutex> lk(ctx->mu);
+      use_device(ctx);
+      drain(ctx);
+    }
+    ctx_release(ctx);  // the last handle released frees the context
+  });
 }
 
 int th_ctx_info(const th_ctx* ctx, uint32_t* N, uint32_t* L, uint64_t* moduli_out) {
@@ -1006,7 +1196,15 @@ int th_ctx_sync(th_ctx* ctx) {
     need(ctx != nullptr, "null context");
     std::lock_guard<std::mutex> lk(ctx->mu);
     use_device(ctx);
-    wait_stream(ctx);
+    drain(ctx);
+  });
+}
+
+int th_ctx_stats(th_ctx* ctx, uint64_t* redrawn_inputs) {
+  return guarded([&] {
+    need(ctx && redrawn_inputs, "null argument");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    *redrawn_inputs = ctx->redrawn_inputs;
   });
 }
 
@@ -1017,9 +1215,10 @@ int th_ctx_stream(th_ctx* ctx, void** stream) {
   });
 }
 
-#define TH_LOCK(c)                          \
-  need((c) != nullptr, "null context");     \
-  std::lock_guard<std::mutex> _lk((c)->mu); \
+#define TH_LOCK(c)                                                      \
+  need((c) != nullptr, "null context");                                 \
+  need(!(c)->closed.load(), "the context has been freed", TH_ESTATE);  \
+  std::lock_guard<std::mutex> _lk((c)->mu);                             \
   use_device(c)
 
 int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out) {
@@ -1032,10 +1231,16 @@ int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out) {
     draw_ternary(s, N, t.data());  // ciphertext.rs:86
     std::vector<int64_t> v(N);
     for (uint32_t i = 0; i < N; ++i) v[i] = t[i] == 0 ? -1 : (t[i] == 1 ? 0 : 1);  // ciphertext.rs:91-96
-    th_sk* sk = new th_sk{ctx, (uint64_t*)ctx->pool.get(L * poly_bytes(ctx))};
-    OpScope sc(ctx);
-    upload_signed(sc, v, sk->d, L);
-    ntt_strided(ctx, false, sk->d, sk->d, L, L);
+    th_sk* sk = adopt(new th_sk{ctx, nullptr});
+    try {
+      sk->d = (uint64_t*)ctx->pool.get(L * poly_bytes(ctx));
+      OpScope sc(ctx);
+      upload_signed(sc, v, sk->d, L);
+      ntt_strided(ctx, false, sk->d, sk->d, L, L);
+    } catch (...) {
+      drop(sk);
+      throw;
+    }
     *out = sk;
   });
 }
@@ -1052,17 +1257,23 @@ int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, 
       for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
     std::vector<int64_t> e(N);
     draw_gaussian(s, N, e.data());
-    th_pk* pk = new th_pk{ctx, (uint64_t*)ctx->pool.get(2 * L * poly_bytes(ctx))};
-    uint64_t* b = pk->d;
-    uint64_t* ad = pk->d + (size_t)L * N;
-    OpScope sc(ctx);
-    uint64_t* etmp = (uint64_t*)sc.dev(L * poly_bytes(ctx));
-    const uint64_t* a_up = sc.up(a);
-    HIPCHK(hipMemcpyAsync(ad, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
-    upload_signed(sc, e, etmp, L);
-    ntt_strided(ctx, false, ad, ad, L, L);
-    ntt_strided(ctx, false, etmp, etmp, L, L);
-    HIPCHK(launch_sub_product(etmp, ad, sk->d, b, ctx->d_bc, N, L, ctx->stream));  // b = e - a*s
+    th_pk* pk = adopt(new th_pk{ctx, nullptr});
+    try {
+      pk->d = (uint64_t*)ctx->pool.get(2 * L * poly_bytes(ctx));
+      uint64_t* b = pk->d;
+      uint64_t* ad = pk->d + (size_t)L * N;
+      OpScope sc(ctx);
+      uint64_t* etmp = (uint64_t*)sc.dev(L * poly_bytes(ctx));
+      const uint64_t* a_up = sc.up(a);
+      HIPCHK(hipMemcpyAsync(ad, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
+      upload_signed(sc, e, etmp, L);
+      ntt_strided(ctx, false, ad, ad, L, L);
+      ntt_strided(ctx, false, etmp, etmp, L, L);
+      HIPCHK(launch_sub_product(etmp, ad, sk->d, b, ctx->d_bc, N, L, ctx->stream));  // b = e - a*s
+    } catch (...) {
+      drop(pk);
+      throw;
+    }
     *out = pk;
   });
 }
@@ -1070,18 +1281,16 @@ int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, 
 int th_sk_free(th_sk* sk) {
   return guarded([&] {
     if (!sk) return;
-    if (sk->dm) sk->ctx->pool.put(sk->dm);
-    sk->ctx->pool.put(sk->d);
-    delete sk;
+    settle_before_free(sk->ctx, sk);
+    drop(sk);
   });
 }
 
 int th_pk_free(th_pk* pk) {
   return guarded([&] {
     if (!pk) return;
-    if (pk->dp) pk->ctx->pool.put(pk->dp);
-    pk->ctx->pool.put(pk->d);
-    delete pk;
+    settle_before_free(pk->ctx, pk);
+    drop(pk);
   });
 }
 
@@ -1128,8 +1337,7 @@ th_ct* encrypt_sk_one(th_ctx* ctx, const th_sk* sk, const std::vector<double>& p
     ntt_strided(ctx, false, c1, c1, L, L);
     HIPCHK(launch_sub_product(me, c1, sk->d, c0, ctx->d_bc, N, L, ctx->stream));  // c0 = (m + e) - a*s
   } catch (...) {
-    ctx->pool.put(ct->d);
-    delete ct;
+    drop(ct);
     throw;
   }
   return ct;
@@ -1164,11 +1372,7 @@ int th_encrypt_batch(th_ctx* ctx, const th_sk* sk, const double* z, const uint64
         made.push_back(encrypt_sk_one(ctx, sk, pad, s));
       }
     } catch (...) {
-      for (th_ct* ct : made) {
-        ctx->pool.put(ct->d);
-        delete ct;
-      }
-      throw;
+      drop_all_rethrow(made);
     }
     for (size_t i = 0; i < count; ++i) outs[i] = made[i];
   });
@@ -1203,7 +1407,7 @@ int th_encrypt_pk_explicit(th_ctx* ctx, const th_pk* pk, const double* z, size_t
     for (uint32_t i = 0; i < N; ++i) need(u[i] <= 2, "u values must be in {0, 1, 2}");
     std::vector<double> pad(N / 2);
     pad_input(ctx, z, n, pad.data());
-    encrypt_pk_many(ctx, pk, pad.data(), 1, nullptr, u, e0, e1, out);
+    encrypt_pk_explicit_many(ctx, pk, pad.data(), 1, u, e0, e1, out);
   });
 }
 
@@ -1232,6 +1436,10 @@ int th_ctx_set_option(th_ctx* ctx, int option, int64_t value) {
       case TH_OPT_FORCE_SERIAL_SAMPLER:
         ctx->force_serial = value != 0;
         break;
+      case TH_OPT_SAMPLER_BAND:
+        need(value >= -52 && value <= -1, "sampler band must be 2^v for v in [-52, -1]");
+        ctx->band = std::ldexp(1.0, (int)value);
+        break;
       default:
         raise(TH_EINVAL, "unknown option " + std::to_string(option));
     }
@@ -1249,9 +1457,7 @@ int th_encode_to_ntt(th_ctx* ctx, const double* z, size_t n, th_pt** out) {
 
 int th_pt_free(th_pt* pt) {
   return guarded([&] {
-    if (!pt) return;
-    pt->ctx->pool.put(pt->d);
-    delete pt;
+    if (pt) drop(pt);
   });
 }
 
@@ -1274,12 +1480,10 @@ int th_ct_pt_mul(th_ctx* ctx, const th_ct* ct, const double* pt, size_t n, th_ct
       const th_pt* ps[1] = {p};
       ct_pt_many(ctx, cs, ps, 1, out);
     } catch (...) {
-      ctx->pool.put(p->d);
-      delete p;
+      drop(p);
       throw;
     }
-    ctx->pool.put(p->d);
-    delete p;
+    drop(p);
   });
 }
 
@@ -1404,32 +1608,48 @@ int th_lora_a_pass(th_ctx* ctx, const th_pk* pk, const th_sk* sk, const double* 
     uint64_t* cts = (uint64_t*)sc.dev(n_inputs * ctb);
     std::vector<uint64_t*> ct_ptr(n_inputs);
     for (uint32_t i = 0; i < n_inputs; ++i) ct_ptr[i] = cts + (size_t)i * 2 * L * N;
-    queue_encrypt_pk(sc, pk, z, n_inputs, seeds, d, cols, ct_ptr.data());
-    // products ct[pt_input[j]] x pts[j] (inference_engine.py:1311)
-    std::vector<CtView> in(n_pts), views(n_pts);
-    std::vector<const uint64_t*> p(n_pts);
-    for (uint32_t j = 0; j < n_pts; ++j) {
-      in[j] = CtView{ct_ptr[pt_input[j]], L, kScale};
-      p[j] = pts[j]->d;
-    }
-    if (do_rescale) {
-      // the product is formed inside the rescale's inverse transforms
-      uint64_t* res = (uint64_t*)sc.dev(n_pts * 2 * (L - 1) * poly_bytes(ctx));
-      std::vector<uint64_t*> rdst(n_pts);
-      for (uint32_t j = 0; j < n_pts; ++j) rdst[j] = res + (size_t)j * 2 * (L - 1) * N;
-      queue_rescale(sc, in, rdst.data(), p.data());
-      for (uint32_t j = 0; j < n_pts; ++j) views[j] = CtView{rdst[j], L - 1, kScale * kScale / (double)ctx->q[L - 1]};
-    } else {
-      uint64_t* prods = (uint64_t*)sc.dev(n_pts * ctb);
-      std::vector<uint64_t*> dst(n_pts);
-      for (uint32_t j = 0; j < n_pts; ++j) {
-        dst[j] = prods + (size_t)j * 2 * L * N;
-        views[j] = CtView{dst[j], L, kScale * kScale};
-      }
-      queue_ct_pt(sc, in, p.data(), dst.data());
-    }
     double* seg = (double*)sc.dev((size_t)n_pts * cols * 8);
-    queue_decrypt(sc, views, sk, nullptr, seg, d, cols);
+    // the whole pass, randomness from the device sampler or from the host
+    auto queue_pass = [&](bool host_draw, BandArgs band) {
+      queue_encrypt_pk(sc, pk, z, n_inputs, seeds, d, cols, ct_ptr.data(), host_draw, band);
+      // products ct[pt_input[j]] x pts[j] (inference_engine.py:1311)
+      std::vector<CtView> in(n_pts), views(n_pts);
+      std::vector<const uint64_t*> p(n_pts);
+      for (uint32_t j = 0; j < n_pts; ++j) {
+        in[j] = CtView{ct_ptr[pt_input[j]], L, kScale};
+        p[j] = pts[j]->d;
+      }
+      if (do_rescale) {
+        // the product is formed inside the rescale's inverse transforms
+        uint64_t* res = (uint64_t*)sc.dev(n_pts * 2 * (L - 1) * poly_bytes(ctx));
+        std::vector<uint64_t*> rdst(n_pts);
+        for (uint32_t j = 0; j < n_pts; ++j) rdst[j] = res + (size_t)j * 2 * (L - 1) * N;
+        queue_rescale(sc, in, rdst.data(), p.data());
+        for (uint32_t j = 0; j < n_pts; ++j)
+          views[j] = CtView{rdst[j], L - 1, kScale * kScale / (double)ctx->q[L - 1]};
+      } else {
+        uint64_t* prods = (uint64_t*)sc.dev(n_pts * ctb);
+        std::vector<uint64_t*> dst(n_pts);
+        for (uint32_t j = 0; j < n_pts; ++j) {
+          dst[j] = prods + (size_t)j * 2 * L * N;
+          views[j] = CtView{dst[j], L, kScale * kScale};
+        }
+        queue_ct_pt(sc, in, p.data(), dst.data());
+      }
+      queue_decrypt(sc, views, sk, nullptr, seg, d, cols);
+    };
+    if (ctx->host_sampler) {
+      queue_pass(true, BandArgs{nullptr, 0.0});
+    } else {
+      const uint32_t off = take_flags(ctx, n_inputs);
+      queue_pass(false, band_args(ctx, off));
+      wait_stream(ctx);
+      if (any_flag(ctx, off, n_inputs)) {  // glibc draws
+        queue_pass(true, BandArgs{nullptr, 0.0});
+        ctx->redrawn_inputs += n_inputs;
+      }
+      release_flags(ctx, off);
+    }
     download(ctx, out, seg, (size_t)n_pts * cols * 8);
   });
 }
@@ -1664,8 +1884,94 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
 }
 
 void free_lora(th_lora* set) {
-  for (void* p : set->owned) set->ctx->pool.put(p);
+  th_ctx* c = set->ctx;
+  for (void* p : set->owned) c->pool.put(p);
   delete set;
+  ctx_release(c);
+}
+
+// Queue one token of the set (the body of th_lora_deltas): encrypt_pk of every
+// input z (device, n_in x d) with randomness from the device sampler (band
+// flags `band`) or, with host_draw, drawn on the host with glibc; ct x pt
+// inside the rescale's transforms; decrypt with segment sums; B applied into
+// dout (device, n_deltas).
+void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* z,
+                 const uint64_t* seeds, int do_rescale, double* dout, bool host_draw, BandArgs band) {
+  const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
+  hipStream_t st = ctx->stream;
+  // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
+  // the encoder launch (next on the stream) finishes the sampler's rejection
+  // check when every input's seed fits one launch
+  const bool fix_in_encode = !host_draw && ni <= SEEDS_PER_LAUNCH;
+  if (host_draw) {
+    OpScope sc(ctx);
+    upload_host_draws(sc, seeds, ni, set->u, set->e0, set->e1);
+  } else {
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, fix_in_encode, band));
+  }
+  HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                       ctx->d_stage_im, ctx->logn, L, st, z, fix_in_encode ? set->d_sample : nullptr, seeds,
+                       ctx->force_serial, band));
+  {
+    NttArgs ea{};
+    ea.lc = ctx->d_lc;
+    ea.jobs = set->d_enc_ntt;
+    ea.load = NTT_LOAD_ENC;
+    ea.bc = ctx->d_bc;
+    bool combined = false;
+    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk_pairs(ctx, pk), set->cts, &combined, st));
+    if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
+  }
+  if (do_rescale) {
+    // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
+    NttArgs ia{}, fa{};
+    ia.lc = fa.lc = ctx->d_lc;
+    ia.bc = fa.bc = ctx->d_bc;
+    ia.jobs = set->d_inv_mul;
+    ia.load = NTT_LOAD_MULM;
+    fa.jobs = set->d_fwd_rs;
+    fa.load = NTT_LOAD_REDUCE;
+    fa.store = NTT_STORE_MUL_RESCALE;
+    fa.rc = ctx->d_rc + (size_t)L * L;
+    HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
+    if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+  } else {
+    HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
+    launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+  }
+  const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
+  if (do_rescale && set->d_dot_seg)
+    launch_dot_segsum(ctx, set->d_dot_seg, nb, sk, set->seg_p, set->cols);
+  else if (set->seg_w)
+    HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));
+  else
+    HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                         ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
+  HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
+}
+
+void resolve_pending(th_ctx* c) {
+  size_t first = c->pending.size();
+  for (size_t i = 0; i < c->pending.size(); ++i)
+    if (any_flag(c, c->pending[i].flag_off, c->pending[i].set->n_in)) {
+      first = i;
+      break;
+    }
+  std::vector<AsyncToken> redo(c->pending.begin() + (std::ptrdiff_t)first, c->pending.end());
+  std::vector<char> flagged(redo.size());
+  for (size_t i = 0; i < redo.size(); ++i) flagged[i] = any_flag(c, redo[i].flag_off, redo[i].set->n_in);
+  c->pending.clear();
+  c->bflag_used = 0;
+  if (redo.empty()) return;
+  // flagged tokens from glibc draws; the others again from the device
+  // sampler, which reproduces their (unflagged) draws exactly
+  for (size_t i = 0; i < redo.size(); ++i) {
+    const AsyncToken& t = redo[i];
+    queue_token(c, t.set, t.pk, t.sk, t.hidden, t.seeds.data(), t.do_rescale, t.deltas, flagged[i] != 0,
+                BandArgs{nullptr, 0.0});
+    if (flagged[i]) c->redrawn_inputs += t.set->n_in;
+  }
+  wait_stream(c);
 }
 
 }  // namespace
@@ -1693,6 +1999,7 @@ int th_lora_create_moe(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_pr
     }
     th_lora* set = new th_lora{};
     set->ctx = ctx;
+    ctx_retain(ctx);
     set->n_in = n_inputs;
     set->d = d;
     set->n_proj = n_proj;
@@ -1717,10 +2024,12 @@ int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, 
 int th_lora_free(th_lora* set) {
   return guarded([&] {
     if (!set) return;
-    std::lock_guard<std::mutex> lk(set->ctx->mu);
-    use_device(set->ctx);
-    HIPCHK(hipStreamSynchronize(set->ctx->stream));
-    free_lora(set);
+    {
+      std::lock_guard<std::mutex> lk(set->ctx->mu);
+      use_device(set->ctx);
+      drain(set->ctx);  // queued tokens of this set are settled (and finished) first
+    }
+    free_lora(set);  // may release the context's last reference: outside its lock
   });
 }
 
@@ -1741,8 +2050,12 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     need(set && set->ctx == ctx, "LoRA set belongs to another context");
     need(pk && pk->ctx == ctx && sk && sk->ctx == ctx, "keys belong to another context");
     need(hidden && seeds && deltas, "null argument");
-    const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
+    const uint32_t L = ctx->L, ni = set->n_in, nb = set->n_batches;
     need(!do_rescale || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
+    const bool async = hidden_on_device && deltas_on_device && !inter;
+    // tokens queued asynchronously before are settled first, so that a redo
+    // of one of them cannot overwrite this call's results
+    if (!async && !ctx->pending.empty()) drain(ctx);
     const size_t hbytes = (size_t)ni * set->d * 8;
     hipStream_t st = ctx->stream;
     // device-resident inputs are read where they are; host inputs go through one copy
@@ -1753,51 +2066,24 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       HIPCHK(hipMemcpyAsync(set->hidden, h, hbytes, hipMemcpyHostToDevice, st));
       z = set->hidden;
     }
-    // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
-    // the encoder launch (next on the stream) finishes the sampler's rejection
-    // check when every input's seed fits one launch
-    const bool fix_in_encode = ni <= SEEDS_PER_LAUNCH;
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, fix_in_encode));
-    HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                         ctx->d_stage_im, ctx->logn, L, st, z, fix_in_encode ? set->d_sample : nullptr, seeds,
-                         ctx->force_serial));
-    {
-      NttArgs ea{};
-      ea.lc = ctx->d_lc;
-      ea.jobs = set->d_enc_ntt;
-      ea.load = NTT_LOAD_ENC;
-      ea.bc = ctx->d_bc;
-      bool combined = false;
-      HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk_pairs(ctx, pk), set->cts, &combined, st));
-      if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
-    }
-    if (do_rescale) {
-      // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
-      NttArgs ia{}, fa{};
-      ia.lc = fa.lc = ctx->d_lc;
-      ia.bc = fa.bc = ctx->d_bc;
-      ia.jobs = set->d_inv_mul;
-      ia.load = NTT_LOAD_MULM;
-      fa.jobs = set->d_fwd_rs;
-      fa.load = NTT_LOAD_REDUCE;
-      fa.store = NTT_STORE_MUL_RESCALE;
-      fa.rc = ctx->d_rc + (size_t)L * L;
-      HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
-      if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
-    } else {
-      HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
-      launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
-    }
-    const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
-    if (do_rescale && set->d_dot_seg)
-      launch_dot_segsum(ctx, set->d_dot_seg, nb, sk, set->seg_p, set->cols);
-    else if (set->seg_w)
-      HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));
-    else
-      HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
     double* dout = deltas_on_device ? deltas : set->deltas;
-    HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
+    if (ctx->host_sampler) {
+      queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, true, BandArgs{nullptr, 0.0});
+    } else {
+      const uint32_t off = take_flags(ctx, ni);
+      queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, false, band_args(ctx, off));
+      if (async) {
+        ctx->pending.push_back(
+            AsyncToken{set, pk, sk, z, std::vector<uint64_t>(seeds, seeds + ni), do_rescale, deltas, off});
+        return;
+      }
+      wait_stream(ctx);
+      if (any_flag(ctx, off, ni)) {  // a draw in the band: the token again, from glibc draws
+        queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, true, BandArgs{nullptr, 0.0});
+        ctx->redrawn_inputs += ni;
+      }
+      release_flags(ctx, off);
+    }
     const size_t db = set->n_deltas * 8, ib = (size_t)nb * set->cols * 8;
     if (!deltas_on_device || inter) {
       char* hh = (char*)ctx->ring.reserve(db + ib, st);
@@ -1815,9 +2101,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
 
 int th_ct_free(th_ct* ct) {
   return guarded([&] {
-    if (!ct) return;
-    ct->ctx->pool.put(ct->d);
-    delete ct;
+    if (ct) drop(ct);
   });
 }
 
@@ -1851,11 +2135,16 @@ int th_ct_upload(th_ctx* ctx, const uint64_t* c0, const uint64_t* c1, uint32_t l
         need(c0[(size_t)l * ctx->N + i] < ctx->q[l] && c1[(size_t)l * ctx->N + i] < ctx->q[l],
              "residues must be reduced modulo their limb prime");
     th_ct* ct = new_ct(ctx, limbs, scale);
-    OpScope sc(ctx);
-    const uint64_t* u0 = (const uint64_t*)sc.upload(c0, ln * 8);
-    const uint64_t* u1 = (const uint64_t*)sc.upload(c1, ln * 8);
-    HIPCHK(hipMemcpyAsync(ct->d, u0, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
-    HIPCHK(hipMemcpyAsync(ct->d + ln, u1, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    try {
+      OpScope sc(ctx);
+      const uint64_t* u0 = (const uint64_t*)sc.upload(c0, ln * 8);
+      const uint64_t* u1 = (const uint64_t*)sc.upload(c1, ln * 8);
+      HIPCHK(hipMemcpyAsync(ct->d, u0, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
+      HIPCHK(hipMemcpyAsync(ct->d + ln, u1, ln * 8, hipMemcpyDeviceToDevice, ctx->stream));
+    } catch (...) {
+      drop(ct);
+      throw;
+    }
     *out = ct;
   });
 }
@@ -1919,10 +2208,16 @@ int th_pk_import(th_ctx* ctx, const uint8_t* buf, size_t len, th_pk** out) {
         need(b < ctx->q[l] && a < ctx->q[l], "residues must be reduced modulo their limb prime");
       }
     (void)w;
-    th_pk* pk = new th_pk{ctx, (uint64_t*)ctx->pool.get(2 * pb)};
-    OpScope sc(ctx);
-    const void* up = sc.upload(buf, 2 * pb);
-    HIPCHK(hipMemcpyAsync(pk->d, up, 2 * pb, hipMemcpyDeviceToDevice, ctx->stream));
+    th_pk* pk = adopt(new th_pk{ctx, nullptr});
+    try {
+      pk->d = (uint64_t*)ctx->pool.get(2 * pb);
+      OpScope sc(ctx);
+      const void* up = sc.upload(buf, 2 * pb);
+      HIPCHK(hipMemcpyAsync(pk->d, up, 2 * pb, hipMemcpyDeviceToDevice, ctx->stream));
+    } catch (...) {
+      drop(pk);
+      throw;
+    }
     *out = pk;
   });
 }
@@ -1947,14 +2242,19 @@ int th_dev_alloc(th_ctx* ctx, size_t bytes, void** out) {
   return guarded([&] {
     TH_LOCK(ctx);
     need(out != nullptr, "null output");
-    *out = ctx->pool.get(bytes);
+    void* p = ctx->pool.get(bytes);
+    ctx->user_allocs.insert(p);
+    *out = p;
   });
 }
 
+// Only buffers from th_dev_alloc that are still held may be freed: a second
+// free, or a ciphertext's or key's own buffer, is refused (the pool would
+// otherwise hand one buffer to two later owners).
 int th_dev_free(th_ctx* ctx, void* p) {
   return guarded([&] {
     TH_LOCK(ctx);
-    need(ctx->pool.owns(p), "pointer was not allocated by th_dev_alloc");
+    need(ctx->user_allocs.erase(p) == 1, "pointer was not allocated by th_dev_alloc, or was already freed");
     ctx->pool.put(p);
   });
 }
@@ -1970,6 +2270,7 @@ int th_memcpy_h2d(th_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int th_memcpy_d2h(th_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guarded([&] {
     TH_LOCK(ctx);
+    if (!ctx->pending.empty()) drain(ctx);  // queued tokens settled before their outputs are read
     HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
   });

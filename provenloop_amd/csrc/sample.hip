@@ -14,15 +14,18 @@
 // kernel regenerates the u words; if any is 0 it replays the whole stream
 // serially, exactly as the reference consumes it.
 //
-// Box-Muller uses the device log/cos; its rounded integer equals glibc's
-// unless the two libraries' results straddle a .5 boundary (an event of
-// probability ~1e-15 per sample). Parity runs use host-supplied randomness.
+// Box-Muller uses the device log/cos. Its rounded integer equals glibc's
+// unless z * 3.19 lies within a few ulps of a .5 boundary; every draw within
+// the band (BandArgs, default 2^-36) of a boundary raises its job's band flag
+// in host-visible memory, and the host redraws that job's randomness with
+// glibc before the result is returned, so the draws equal the reference's.
 #include "sample_device.h"
 
 namespace th {
 
 // One thread per 16-word block of the stream.
-__global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, SeedBlock sb, int use_sb) {
+__global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, SeedBlock sb, int use_sb,
+                                BandArgs band) {
   const SampleJob jb = jobs[blockIdx.y];
   const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.y);
   const uint32_t nblocks = 9 * (n / 16);
@@ -40,22 +43,26 @@ __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, 
     if (zero && jb.reject) atomicOr(jb.reject, 1u);  // range_u32 rejects 0 (rng.rs:112-119)
   } else {
     const uint32_t g0 = (16 * b - n) / 4;
+    bool any = false;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t g = g0 + t;
-      const int64_t e = gaussian_rounded(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3]);
+      bool near;
+      const int64_t e = gaussian_rounded(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3], band.band, near);
+      any |= near;
       if (g < n)
         gst(jb.e0)[g] = e;
       else
         gst(jb.e1)[g - n] = e;
     }
+    if (any && band.flags) band.flags[blockIdx.y] = 1;  // a plain store; rare
   }
 }
 
 // One workgroup per job: re-derive the u words; if any was rejected (== 0),
 // or force_serial is set, lane 0 rewrites u, e0 and e1 by the serial walk.
 __global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restrict__ jobs, uint32_t n, int force_serial,
-                                                      SeedBlock sb, int use_sb) {
+                                                      SeedBlock sb, int use_sb, BandArgs band) {
   const SampleJob jb = jobs[blockIdx.x];
   const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.x);
   int bad = 0;
@@ -67,21 +74,21 @@ __global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restric
   }
   bad = __syncthreads_or(bad) | force_serial;
   if (!bad || threadIdx.x != 0) return;
-  serial_replay(jb, seed, n);
+  serial_replay(jb, seed, n, band.flags ? band.flags + blockIdx.x : nullptr, band.band);
 }
 
 // One thread per job with a reject flag: replay flagged (or forced) jobs
 // serially, then clear the flag for the next launch.
 __global__ void k_sample_fix(const SampleJob* __restrict__ jobs, uint32_t njobs, uint32_t n, int force_serial,
-                             SeedBlock sb, int use_sb) {
+                             SeedBlock sb, int use_sb, BandArgs band) {
   const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= njobs) return;
   const SampleJob jb = jobs[j];
-  sample_fix_job(jb, job_seed(jb, sb, use_sb, j), n, force_serial);
+  sample_fix_job(jb, job_seed(jb, sb, use_sb, j), n, force_serial, band.flags ? band.flags + j : nullptr, band.band);
 }
 
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
-                            const uint64_t* seeds, bool flagged, bool fix_later) {
+                            const uint64_t* seeds, bool flagged, bool fix_later, BandArgs band) {
   if (!njobs) return hipSuccess;
   if (n % 16) return hipErrorInvalidValue;
   const uint32_t nblocks = 9 * (n / 16);
@@ -90,16 +97,17 @@ hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, i
     const uint32_t cnt = njobs - first < SEEDS_PER_LAUNCH ? njobs - first : SEEDS_PER_LAUNCH;
     if (seeds)
       for (uint32_t i = 0; i < cnt; ++i) sb.v[i] = seeds[first + i];
+    const BandArgs bf{band.flags ? band.flags + first : nullptr, band.band};
     hipLaunchKernelGGL(k_sample_blocks, dim3((nblocks + 255) / 256, cnt), dim3(256), 0, s, jobs + first, n, sb,
-                       seeds != nullptr);
+                       seeds != nullptr, bf);
     if (flagged && fix_later)
       continue;  // the caller's next launch replays flagged jobs and clears the flags
     if (flagged)
       hipLaunchKernelGGL(k_sample_fix, dim3((cnt + 63) / 64), dim3(64), 0, s, jobs + first, cnt, n, force_serial, sb,
-                         seeds != nullptr);
+                         seeds != nullptr, bf);
     else
       hipLaunchKernelGGL(k_sample_check, dim3(cnt), dim3(256), 0, s, jobs + first, n, force_serial, sb,
-                         seeds != nullptr);
+                         seeds != nullptr, bf);
   }
   return hipGetLastError();
 }

@@ -38,12 +38,27 @@ static __device__ __forceinline__ double unit_open(uint32_t w0, uint32_t w1) {
   return ((double)(v >> 11) + 0.5) / 9007199254740992.0;     // rng.rs:139-144
 }
 
-static __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+// Where a sample's rounding could depend on the math library: t = z * 3.19
+// within `band` of a rounding boundary k + 1/2, or not finite. The device's
+// log/cos differ from glibc's (which the reference calls through Rust std) by
+// a few ulps, so |t_device - t_glibc| stays below about 2^-45 (|z| < 8.7,
+// |t| < 28); with the default band of 2^-36 every sample whose rounded value
+// could differ from glibc's is flagged, and the host redraws it with glibc.
+// t - floor(t) and the difference from 1/2 are exact for |t| < 2^52.
+static __device__ __forceinline__ bool near_rounding_boundary(double t, double band) {
+  if (!(fabs(t) < 0x1p52)) return true;
+  return fabs((t - floor(t)) - 0.5) < band;
+}
+
+static __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                           double band, bool& near) {
   const double u1 = unit_open(w0, w1);
   const double u2 = unit_open(w2, w3);
   constexpr double kTwoPi = 2.0 * 3.14159265358979323846264338327950288;  // 2.0 * PI, exact doubling
   const double z = sqrt(-2.0 * log(u1)) * cos(kTwoPi * u2);                // rng.rs:155
-  const double r = round(z * 3.19);                                      // sampling.rs:54-55
+  const double t = z * 3.19;
+  near = near_rounding_boundary(t, band);
+  const double r = round(t);  // sampling.rs:54-55
   if (r != r) return 0;
   if (r >= 9223372036854775808.0) return INT64_MAX;
   if (r < -9223372036854775808.0) return INT64_MIN;
@@ -76,28 +91,34 @@ struct SerialStream {
 
 // The reference's consumption order for one stream, walked serially
 // (handles range_u32 rejections: rng.rs:109-133, ciphertext.rs:255-273).
-static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_t n) {
+// flag: this job's band flag (null: none).
+static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_t n, uint8_t* flag, double band) {
   SerialStream st(seed);
   for (uint32_t i = 0; i < n; ++i) {
     uint32_t r = st.next();
     for (uint32_t guard = 0; r < 1 && guard < (1u << 20); ++guard) r = st.next();  // rng.rs:112-119
     jb.u[i] = ternary_value(r);
   }
+  bool any = false;
   for (uint32_t i = 0; i < 2 * n; ++i) {
     const uint32_t w0 = st.next(), w1 = st.next(), w2 = st.next(), w3 = st.next();
-    const int64_t e = gaussian_rounded(w0, w1, w2, w3);
+    bool near;
+    const int64_t e = gaussian_rounded(w0, w1, w2, w3, band, near);
+    any |= near;
     if (i < n)
       jb.e0[i] = e;
     else
       jb.e1[i - n] = e;
   }
+  if (any && flag) *flag = 1;
 }
 
 // The end of a flagged sampler launch for job j: replay the stream serially
 // if a u word was rejected (or force_serial), then clear the flag. Run by one
 // thread, in a launch ordered after the block kernel.
-static __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial) {
-  if (*jb.reject || force_serial) serial_replay(jb, seed, n);
+static __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial, uint8_t* flag,
+                                      double band) {
+  if (*jb.reject || force_serial) serial_replay(jb, seed, n, flag, band);
   *jb.reject = 0;
 }
 

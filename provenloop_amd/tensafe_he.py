@@ -453,6 +453,18 @@ class CkksContext:
             raise ValueError("sampler must be 'device' or 'host'")
         _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_SAMPLER, value))
 
+    def set_sampler_band(self, log2_band: int):
+        """Band of the device sampler's boundary check: Gaussian draws whose
+        z * 3.19 lies within 2**log2_band of a rounding boundary are drawn
+        again on the host with glibc (default -36)."""
+        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_SAMPLER_BAND, int(log2_band)))
+
+    def redrawn_inputs(self) -> int:
+        """How many encrypt_pk inputs the host has drawn again after the band check."""
+        v = C.c_uint64()
+        _lib.check(_lib.load().th_ctx_stats(self._h, C.byref(v)))
+        return v.value
+
     def _force_serial_sampler(self, on: bool):
         """Testing hook: replay every device stream serially (the rejection path)."""
         _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_FORCE_SERIAL_SAMPLER, int(on)))
