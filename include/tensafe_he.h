@@ -182,6 +182,20 @@ int th_batch_decrypt(th_ctx* ctx, const th_ct* const* cts, size_t count, const t
  * one host sync and count x cols doubles per batch. */
 int th_batch_decrypt_segsum(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk, uint32_t d,
                             uint32_t cols, double* out);
+/* th_batch_decrypt_segsum that allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code that
+ * must not call hipMalloc, tight serving loops, allocation-free harnesses).
+ * Job lists, segment weights, decrypted coefficients and partial sums live in
+ * a static 32 MiB device array per GPU (held until the process ends); host
+ * staging uses the context's pinned ring. Results equal
+ * th_batch_decrypt_segsum's. A batch whose working set exceeds the 32 MiB
+ * (about 60 ciphertexts at N = 16384 on the CRT or full-decode paths, far
+ * more on the limb-0 path with at most 8 segments) is refused with TH_EINVAL.
+ * Calls on one GPU share its array: this library runs them one at a time
+ * (a per-device lock held until the call returns), and each call writes
+ * everything it reads in the array before reading it. */
+int th_batch_decrypt_segsum_noalloc(th_ctx* ctx, const th_ct* const* cts, size_t count, const th_sk* sk,
+                                    uint32_t d, uint32_t cols, double* out);
 /* As th_batch_decrypt, writing count x N/2 doubles to device memory at
  * dev_out (e.g. a ROCm torch tensor; the engine's decrypt_to_gpu,
  * inference_engine.py:190-205). The context stream is synchronised before return. */

@@ -64,6 +64,7 @@ _SIGS = {
     "th_batch_decrypt": (I32, [VP, VP, SZ, VP, VP]),
     "th_batch_decrypt_segsum": (I32, [VP, VP, SZ, VP, U32, U32, VP]),
     "th_batch_decrypt_device": (I32, [VP, VP, SZ, VP, VP]),
+    "th_batch_decrypt_segsum_noalloc": (I32, [VP, VP, SZ, VP, U32, U32, VP]),
     "th_lora_a_pass": (I32, [VP, VP, VP, VP, U32, U32, VP, VP, VP, U32, I32, VP]),
     "th_lora_create": (I32, [VP, U32, U32, U32, VP, VP, VP, VP, VP, PVP]),
     "th_lora_create_moe": (I32, [VP, U32, U32, U32, VP, VP, VP, U32, VP, VP, VP, PVP]),

@@ -209,6 +209,8 @@ __global__ void k_segsum_final(const DecodeJob* __restrict__ jobs, uint32_t njob
   gst(jb.seg)[c] = s / jb.scale;
 }
 
+size_t segsum_parts_doubles(uint32_t cols) { return (size_t)SEGSUM_CHUNKS * cols; }
+
 hipError_t launch_segsum(const DecodeJob* jobs, uint32_t njobs, const DecodeConst* dc, const double* W,
                          uint32_t logn, uint32_t cols, hipStream_t s) {
   if (!njobs) return hipSuccess;

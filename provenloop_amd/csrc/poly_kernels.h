@@ -92,6 +92,7 @@ hipError_t launch_decode(const DecodeJob* jobs, uint32_t njobs, const DecodeCons
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t d, uint32_t cols, hipStream_t s);
 size_t decode_parts_doubles(uint32_t logn);  // scratch doubles per job
+size_t segsum_parts_doubles(uint32_t cols);  // scratch doubles per job of launch_segsum
 // Segment sums of the decoded slots taken straight from the decrypted
 // coefficients with segment weights W (cols x N, segment_weights()); each
 // job's `seg` receives cols sums, within rounding of decode-then-sum. Uses
