@@ -96,11 +96,23 @@ __device__ __forceinline__ T ld16(GPtr<T> p, uint32_t i) {
 
 // floor(x * s / 2^64) - e with e in {0, 1, 2}: x1*s1 + hi(x1*s0) + hi(x0*s1)
 // for 32-bit halves; the low halves of the two cross products and hi(x0*s0)
-// are dropped, each below 2^32, so at most 2 is lost after the shift.
+// are dropped, each below 2^32, so at most 2 is lost after the shift. The sum
+// stays below 2^64. The last term goes in as a 32-bit add with carry (two
+// 32-bit instructions): left to the compiler it becomes a zero-extending move
+// and a 64-bit add.
 __device__ __forceinline__ uint64_t mulhi_approx(uint64_t x, uint64_t s) {
   const uint32_t x0 = (uint32_t)x, x1 = (uint32_t)(x >> 32), s0 = (uint32_t)s, s1 = (uint32_t)(s >> 32);
-  const uint64_t h = (uint64_t)__umulhi(x1, s0) + __umulhi(x0, s1);
-  return (uint64_t)x1 * s1 + h;
+  const uint64_t r = (uint64_t)x1 * s1 + __umulhi(x1, s0);
+  uint32_t rl = (uint32_t)r, rh = (uint32_t)(r >> 32);
+  asm("v_add_co_u32 %0, vcc, %0, %2\n\tv_addc_co_u32 %1, vcc, %1, 0, vcc" : "+v"(rl), "+v"(rh) : "v"(__umulhi(x0, s1))
+      : "vcc");
+  return ((uint64_t)rh << 32) | rl;
+}
+
+// v unchanged, hidden from the optimiser (see opaque_u64).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
 }
 
 // x * w mod q in [0, 4q) for any 64-bit x (w < q, ws = floor(w * 2^64 / q)):
@@ -115,7 +127,10 @@ __device__ __forceinline__ uint64_t shoup_approx(uint64_t x, uint64_t w, uint64_
   const uint32_t x0 = (uint32_t)x, x1 = (uint32_t)(x >> 32), w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
   const uint32_t h0 = (uint32_t)qh, h1 = (uint32_t)(qh >> 32), n0 = (uint32_t)nq, n1 = (uint32_t)(nq >> 32);
   const uint64_t lo = (uint64_t)x0 * w0 + (uint64_t)h0 * n0;
-  const uint32_t hi = (uint32_t)(lo >> 32) + x0 * w1 + x1 * w0 + h0 * n1 + h1 * n0;
+  // the high word as one 32-bit sum (the cross products pair up as multiply-
+  // adds); kept opaque so that the compiler does not turn the word assembly
+  // back into a 64-bit add of the shifted cross terms
+  const uint32_t hi = opaque_u32((uint32_t)(lo >> 32) + (x0 * w1 + x1 * w0) + (h0 * n1 + h1 * n0));
   return ((uint64_t)hi << 32) | (uint32_t)lo;
 }
 
