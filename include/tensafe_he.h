@@ -245,6 +245,15 @@ int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, 
 int th_lora_create_moe(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, const uint32_t* input_of,
                        const uint32_t* ranks, const uint32_t* d_out, uint32_t n_experts, const double* gates,
                        const double* const* a, const double* const* b, th_lora** out);
+/* Gates of a set made by th_lora_create_moe with gates, replaced (a gate
+ * that changes per token; no counterpart in the reference, see
+ * th_lora_create_moe). gates: n_proj x n_experts, finite. The experts'
+ * plaintexts g*A are encoded, transformed and folded again and B = sum_x
+ * g_x B_x is mixed again, all on the device and queued on the context's
+ * stream: th_lora_deltas calls made after it use the new gates, bit for bit
+ * as a set created with them. Tokens queued without waiting are settled
+ * first. TH_ESTATE for a set created without gates. */
+int th_lora_set_gates(th_ctx* ctx, th_lora* set, const double* gates);
 int th_lora_free(th_lora* set);
 /* n_deltas = sum of d_out (length of th_lora_deltas' output), n_batches =
  * number of plaintext batches, cols = segments per batch. Any may be NULL. */

@@ -68,6 +68,7 @@ _SIGS = {
     "th_lora_a_pass": (I32, [VP, VP, VP, VP, U32, U32, VP, VP, VP, U32, I32, VP]),
     "th_lora_create": (I32, [VP, U32, U32, U32, VP, VP, VP, VP, VP, PVP]),
     "th_lora_create_moe": (I32, [VP, U32, U32, U32, VP, VP, VP, U32, VP, VP, VP, PVP]),
+    "th_lora_set_gates": (I32, [VP, VP, VP]),
     "th_lora_free": (I32, [VP]),
     "th_lora_info": (I32, [VP, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32)]),
     "th_lora_deltas": (I32, [VP, VP, VP, VP, VP, I32, VP, I32, VP, I32, VP]),

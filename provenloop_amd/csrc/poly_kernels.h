@@ -65,6 +65,26 @@ struct LoraBJob {
 hipError_t launch_lora_b(const LoraBJob* jobs, uint32_t njobs, uint32_t max_d_out, const double* sums, double* out,
                          uint32_t cols, hipStream_t s);
 
+// One plaintext batch of a mixture LoRA set: its projection and how many of
+// its slots hold A rows (rows x d).
+struct MoeBatch {
+  uint32_t proj;
+  uint32_t n_valid;
+};
+// One projection's B in a mixture set: offset of its mixed B (count doubles,
+// rank-major) in the mixed buffer; its k experts' B sit at off * k + x * count.
+struct MoeProj {
+  uint64_t off;
+  uint32_t count;
+  uint32_t pad_;
+};
+// out (nb*k x slots) = gate-scaled packed A rows of every batch and expert (k_moe_gate_pack).
+hipError_t launch_moe_gate_pack(const double* apack, const MoeBatch* batches, const double* gates, uint32_t nb,
+                                uint32_t k, uint32_t slots, double* out, hipStream_t s);
+// bmix = sum_x g_x B_x per projection (k_moe_mix_b).
+hipError_t launch_moe_mix_b(const double* bexp, const MoeProj* projs, const double* gates, uint32_t n_proj, uint32_t k,
+                            uint32_t max_count, double* bmix, hipStream_t s);
+
 hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_limbs, const BarrettConst* bc,
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,

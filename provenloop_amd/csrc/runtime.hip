@@ -281,6 +281,14 @@ struct th_lora {
   uint32_t dot_n_jobs = 0, dot_r_jobs = 0;
   const double* seg_w = nullptr;  // segment weights, or null: decode the slots and sum them
   const double* seg_p = nullptr;  // the same in recurrence form (decrypt transform's epilogue)
+  // gated (mixture) sets: k experts per projection, regated by th_lora_set_gates
+  uint32_t k = 1;
+  const double* apack = nullptr;  // n_batches x k x N/2: the experts' packed A rows, ungated
+  const double* bexp = nullptr;   // the experts' B, rank-major (MoeProj)
+  double* bmix = nullptr;         // sum_x g_x B_x: what the B jobs read
+  const MoeBatch* d_moe_b = nullptr;
+  const MoeProj* d_moe_p = nullptr;
+  uint32_t max_b_count = 0;
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
     owned.push_back(p);
@@ -1841,6 +1849,23 @@ void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, Nt
   HIPCHK(launch_ntt((int)c->logn, inverse, a, n, c->stream));
 }
 
+// Queue the plaintexts and mixed B of a mixture set for the gates g (device,
+// n_proj x k): every batch's k expert plaintexts encode_to_ntt(g_x * A_x rows)
+// (the encoder and transforms of th_encode_to_ntt), folded into one
+// (launch_pt_sum) and its Montgomery form, and B = sum_x g_x B_x.
+void queue_regate(OpScope& sc, th_lora* set, const double* g) {
+  th_ctx* c = sc.c;
+  const uint32_t N = c->N, S = N / 2, L = c->L, nb = set->n_batches, k = set->k;
+  double* z = (double*)sc.dev((size_t)nb * k * S * 8);
+  HIPCHK(launch_moe_gate_pack(set->apack, set->d_moe_b, g, nb, k, S, z, c->stream));
+  uint64_t* dst = (uint64_t*)sc.dev((size_t)nb * k * L * poly_bytes(c));
+  queue_encode(sc, z, (size_t)nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
+  ntt_strided(c, false, dst, dst, nb * k * L, L);
+  HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
+  HIPCHK(launch_to_montgomery(set->pts, set->ptm, c->d_bc, N, L, nb, c->stream));
+  HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, g, set->n_proj, k, set->max_b_count, set->bmix, c->stream));
+}
+
 // k experts per projection. Expert x of projection j has A = a[j * k + x],
 // B = b[j * k + x] and gate weight gates[j * k + x]; gates == nullptr (k == 1)
 // is a plain LoRA set.
@@ -1854,59 +1879,60 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const uint32_t N = c->N, S = N / 2, L = c->L, d = set->d, cols = set->cols;
   const size_t P = poly_bytes(c);
   // plaintext batches (inference_engine.py:1300-1308) and the B jobs
+  // Batches hold the A rows as they are (no gates) or ungated per expert
+  // (gated sets: the gate is applied on the device, queue_regate). B is stored
+  // rank-major on the device (element (i, r) at r * d_out + i), so the B
+  // kernel's lanes, one output row each, read consecutive addresses; with
+  // experts, each one's B in turn (MoeProj), mixed on the device.
+  set->k = k;
   std::vector<double> packed;
   std::vector<uint32_t> batch_input;
+  std::vector<MoeBatch> moe_b;
+  std::vector<MoeProj> moe_p(set->n_proj);
   std::vector<LoraBJob> bj(set->n_proj);
   std::vector<double> bmat;
-  uint64_t out_off = 0;
+  uint64_t out_off = 0, boff = 0;
   for (uint32_t j = 0; j < set->n_proj; ++j) {
     const uint32_t nb = (ranks[j] + cols - 1) / cols;
     bj[j] = LoraBJob{nullptr, d_out[j], ranks[j], (uint32_t)batch_input.size(), 0, out_off};
     for (uint32_t bt = 0; bt < nb; ++bt) {
+      const uint32_t rows = std::min(cols, ranks[j] - bt * cols);
       for (uint32_t x = 0; x < k; ++x) {
         const double* ax = a[(size_t)j * k + x];
         packed.resize(packed.size() + S, 0.0);
         double* p = packed.data() + packed.size() - S;
-        for (uint32_t i = 0; i < cols && bt * cols + i < ranks[j]; ++i) {
-          const double* row = ax + (size_t)(bt * cols + i) * d;
-          if (!gates) {
-            memcpy(p + (size_t)i * d, row, (size_t)d * 8);
-          } else {
-            const double g = gates[(size_t)j * k + x];
-            for (uint32_t t = 0; t < d; ++t) p[(size_t)i * d + t] = g * row[t];
-          }
-        }
+        for (uint32_t i = 0; i < rows; ++i) memcpy(p + (size_t)i * d, ax + (size_t)(bt * cols + i) * d, (size_t)d * 8);
       }
       batch_input.push_back(input_of[j]);
+      moe_b.push_back(MoeBatch{j, rows * d});
     }
     const size_t bn = (size_t)d_out[j] * ranks[j];
-    std::vector<double> mix(b[j], b[j] + bn);
-    if (gates) {
-      std::fill(mix.begin(), mix.end(), 0.0);
-      for (uint32_t x = 0; x < k; ++x) {
-        const double g = gates[(size_t)j * k + x];
-        const double* bx = b[(size_t)j * k + x];
-        for (size_t t = 0; t < bn; ++t) mix[t] += g * bx[t];
-      }
+    moe_p[j] = MoeProj{boff, (uint32_t)bn, 0};
+    for (uint32_t x = 0; x < k; ++x) {
+      const double* bx = b[(size_t)j * k + x];
+      const size_t b0 = bmat.size();
+      bmat.resize(b0 + bn);
+      for (uint32_t i = 0; i < d_out[j]; ++i)
+        for (uint32_t r = 0; r < ranks[j]; ++r) bmat[b0 + (size_t)r * d_out[j] + i] = bx[(size_t)i * ranks[j] + r];
     }
-    // rank-major on the device (element (i, r) at r * d_out + i): the
-    // kernel's lanes, one output row each, then read consecutive addresses
-    const size_t b0 = bmat.size();
-    bmat.resize(b0 + bn);
-    for (uint32_t i = 0; i < d_out[j]; ++i)
-      for (uint32_t r = 0; r < ranks[j]; ++r) bmat[b0 + (size_t)r * d_out[j] + i] = mix[(size_t)i * ranks[j] + r];
+    boff += bn;
     out_off += d_out[j];
     set->max_d_out = std::max(set->max_d_out, d_out[j]);
+    set->max_b_count = std::max(set->max_b_count, (uint32_t)bn);
   }
   set->n_batches = (uint32_t)batch_input.size();
   set->n_deltas = out_off;
   const uint32_t nb = set->n_batches, ni = set->n_in;
-  const double* d_b = persist(set, bmat);
-  size_t boff = 0;
-  for (uint32_t j = 0; j < set->n_proj; ++j) {
-    bj[j].b = d_b + boff;
-    boff += (size_t)d_out[j] * ranks[j];
+  const bool gated = gates != nullptr;
+  if (!gated) {
+    set->bmix = const_cast<double*>(persist(set, bmat));
+  } else {
+    set->bexp = persist(set, bmat);
+    set->bmix = (double*)set->alloc((size_t)boff * 8);
+    set->d_moe_b = persist(set, moe_b);
+    set->d_moe_p = persist(set, moe_p);
   }
+  for (uint32_t j = 0; j < set->n_proj; ++j) bj[j].b = set->bmix + moe_p[j].off;
   // device memory
   set->pts = (uint64_t*)set->alloc(nb * L * P);
   set->ptm = (uint64_t*)set->alloc(nb * L * P);
@@ -1937,16 +1963,18 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->d_comb = persist(set, cj);
   }
   // encode the plaintext batches (th_encode_to_ntt of each packed vector); with
-  // experts, fold each batch's k plaintexts into one
-  {
+  // gates, the gated batches, folded (queue_regate)
+  if (!gated) {
     OpScope sc(c);
-    const double* z = sc.up(packed);
-    uint64_t* dst = k == 1 ? set->pts : (uint64_t*)sc.dev((size_t)nb * k * L * P);
-    queue_encode(sc, z, nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
-    ntt_strided(c, false, dst, dst, nb * k * L, L);
-    if (k > 1) HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
+    queue_encode(sc, sc.up(packed), nb, nullptr, nullptr, nullptr, set->pts, (size_t)L * N);
+    ntt_strided(c, false, set->pts, set->pts, nb * L, L);
     HIPCHK(launch_to_montgomery(set->pts, set->ptm, c->d_bc, N, L, nb, c->stream));
     HIPCHK(hipStreamSynchronize(c->stream));  // the scope's buffers return to the pool
+  } else {
+    set->apack = persist(set, packed);
+    OpScope sc(c);
+    queue_regate(sc, set, sc.up(std::vector<double>(gates, gates + (size_t)set->n_proj * k)));
+    HIPCHK(hipStreamSynchronize(c->stream));
   }
   // per-token job lists
   std::vector<EncodeJob> ej(ni);
@@ -2176,6 +2204,21 @@ int th_lora_create(th_ctx* ctx, uint32_t n_inputs, uint32_t d, uint32_t n_proj, 
                    const uint32_t* ranks, const uint32_t* d_out, const double* const* a, const double* const* b,
                    th_lora** out) {
   return th_lora_create_moe(ctx, n_inputs, d, n_proj, input_of, ranks, d_out, 1, nullptr, a, b, out);
+}
+
+int th_lora_set_gates(th_ctx* ctx, th_lora* set, const double* gates) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(set && set->ctx == ctx, "LoRA set belongs to another context");
+    need(set->apack != nullptr, "the LoRA set was created without gates", TH_ESTATE);
+    need(gates != nullptr, "null gates");
+    const size_t ng = (size_t)set->n_proj * set->k;
+    for (size_t i = 0; i < ng; ++i) need(std::isfinite(gates[i]), "gate weights must be finite");
+    // a queued token redone later (sampler band) must see the plaintexts it was queued with
+    if (!ctx->pending.empty()) drain(ctx);
+    OpScope sc(ctx);
+    queue_regate(sc, set, sc.up(std::vector<double>(gates, gates + ng)));
+  });
 }
 
 int th_lora_free(th_lora* set) {

@@ -149,7 +149,8 @@ class LoraSet:
     projection). Each batch's ciphertext is then the ct_add of the k
     experts' products with their gate-scaled plaintexts g_x A_x, so the
     decrypted intermediate is sum_x g_x A_x h, and the deltas are
-    (sum_x g_x B_x) @ intermediate.
+    (sum_x g_x B_x) @ intermediate. `set_gates()` replaces the gates (a gate
+    that changes per token) on the device.
     """
 
     def __init__(self, ctx: CkksContext, n_inputs: int, projections, gates=None):
@@ -206,6 +207,16 @@ class LoraSet:
         if h and _lib._lib is not None:
             _lib._lib.th_lora_free(h)
             self._h = None
+
+    def set_gates(self, gates):
+        """Replace the gates [n_proj, k] of a set created with gates
+        (th_lora_set_gates): queued on the context stream, so the next
+        deltas()/deltas_device() call uses them, bit for bit as a set created
+        with these gates."""
+        G = np.ascontiguousarray(gates, np.float64)
+        if G.shape != (len(self.d_out), self.n_experts):
+            raise ValueError(f"gates must be [{len(self.d_out)}, {self.n_experts}]")
+        _lib.check(self._lib.th_lora_set_gates(self._ctx._h, self._h, _lib.ptr(G)))
 
     def deltas(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden, seeds, rescale: bool = True,
                with_intermediates: bool = False):

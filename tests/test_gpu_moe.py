@@ -133,3 +133,63 @@ def test_moe_argument_errors(env):
         zero_moai.LoraSet(eng, 1, proj, gates=bad)
     with pytest.raises(ValueError):
         zero_moai.LoraSet(eng, 1, [(0, proj[0][1][0], proj[0][2][0])], gates=gates)  # 2-D A with gates
+
+
+def test_moe_set_gates_equals_set_created_with_them(env):
+    """A gate that changes per token (th_lora_set_gates): after regating, the set's deltas and
+    segment sums equal, bit for bit, those of a set created with the new gates, and the old
+    gates come back exactly."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(25)
+    H = rng.normal(size=(2, 1536)) * 0.1
+    proj, g1 = _experts(rng, 2)
+    g2 = np.array([zero_moai.softmax_gate(777 + j, K) for j in range(len(proj))])
+    ls = zero_moai.LoraSet(eng, 2, proj, gates=g1)
+    a1, s1 = ls.deltas(pk, sk, H, [91, 92], with_intermediates=True)
+    ls.set_gates(g2)
+    a2, s2 = ls.deltas(pk, sk, H, [91, 92], with_intermediates=True)
+    fresh = zero_moai.LoraSet(eng, 2, proj, gates=g2)
+    b2, t2 = fresh.deltas(pk, sk, H, [91, 92], with_intermediates=True)
+    assert np.array_equal(s2, t2)
+    for x, y in zip(a2, b2):
+        assert np.array_equal(x, y)
+    assert not np.array_equal(s1, s2)
+    ls.set_gates(g1)
+    a3, s3 = ls.deltas(pk, sk, H, [91, 92], with_intermediates=True)
+    assert np.array_equal(s1, s3)
+    for x, y in zip(a1, a3):
+        assert np.array_equal(x, y)
+
+
+def test_moe_set_gates_matches_oracle_per_token(env):
+    """Three tokens, each with its own seeded gate, against the oracle's literal k products +
+    ct_add + rescale + decrypt with that token's gates (layer 0, q and v)."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(26)
+    proj, g0 = _experts(rng, 1)
+    ls = zero_moai.LoraSet(eng, 1, proj, gates=g0)
+    for t in range(3):
+        H = rng.normal(size=(1, 1536)) * 0.1
+        gt = np.array([zero_moai.softmax_gate(100 * t + j, K) for j in range(len(proj))])
+        ls.set_gates(gt)
+        got, got_sums = ls.deltas(pk, sk, H, [200 + t], with_intermediates=True)
+        exp, exp_sums = _oracle(ref, rpk, rsk, H, [200 + t], proj, gt)
+        assert np.max(np.abs(got_sums - exp_sums)) <= 1e-9 * max(1.0, np.max(np.abs(exp_sums)))
+        for g, e in zip(got, exp):
+            assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e)
+
+
+def test_moe_set_gates_errors(env):
+    eng = env[0]
+    rng = np.random.default_rng(27)
+    proj, gates = _experts(rng, 1, d_outs=(8,))
+    ls = zero_moai.LoraSet(eng, 1, proj, gates=gates)
+    with pytest.raises(ValueError):
+        ls.set_gates(gates[:, :2])
+    bad = gates.copy()
+    bad[0, 1] = np.inf
+    with pytest.raises(ValueError, match="finite"):
+        ls.set_gates(bad)
+    plain = zero_moai.LoraSet(eng, 1, [(0, proj[0][1][0], proj[0][2][0])])
+    with pytest.raises(RuntimeError, match="without gates"):
+        plain.set_gates(np.ones((1, 1)))
