@@ -1850,9 +1850,11 @@ void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, Nt
 }
 
 // Queue the plaintexts and mixed B of a mixture set for the gates g (device,
-// n_proj x k): every batch's k expert plaintexts encode_to_ntt(g_x * A_x rows)
-// (the encoder and transforms of th_encode_to_ntt), folded into one
-// (launch_pt_sum) and its Montgomery form, and B = sum_x g_x B_x.
+// n_proj x k): every batch's plaintext is sum_x encode_to_ntt(g_x * A_x rows)
+// (the encoder and transforms of th_encode_to_ntt), then its Montgomery form,
+// and B = sum_x g_x B_x. The transform is linear mod q, so the k encoded
+// residue polynomials are summed first (launch_pt_sum) and transformed once
+// per batch and limb: the same residues as summing the k transforms.
 void queue_regate(OpScope& sc, th_lora* set, const double* g) {
   th_ctx* c = sc.c;
   const uint32_t N = c->N, S = N / 2, L = c->L, nb = set->n_batches, k = set->k;
@@ -1860,8 +1862,8 @@ void queue_regate(OpScope& sc, th_lora* set, const double* g) {
   HIPCHK(launch_moe_gate_pack(set->apack, set->d_moe_b, g, nb, k, S, z, c->stream));
   uint64_t* dst = (uint64_t*)sc.dev((size_t)nb * k * L * poly_bytes(c));
   queue_encode(sc, z, (size_t)nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
-  ntt_strided(c, false, dst, dst, nb * k * L, L);
   HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
+  ntt_strided(c, false, set->pts, set->pts, nb * L, L);
   HIPCHK(launch_to_montgomery(set->pts, set->ptm, c->d_bc, N, L, nb, c->stream));
   HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, g, set->n_proj, k, set->max_b_count, set->bmix, c->stream));
 }
