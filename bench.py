@@ -100,8 +100,9 @@ class DeviceInputs:
         _lib.check(self.L.th_memcpy_h2d(ctx._h, self.h, _lib.ptr(Hs), Hs.nbytes))
         ctx.sync()
 
-    def run(self, pk, sk, step, seeds):
-        self.lora.deltas_device(pk, sk, self.h.value + step * self.h_stride, seeds, self.o.value + step * self.o_stride)
+    def run(self, pk, sk, step, seeds, rescale=True):
+        self.lora.deltas_device(pk, sk, self.h.value + step * self.h_stride, seeds, self.o.value + step * self.o_stride,
+                                rescale=rescale)
 
     def deltas(self, step):
         from provenloop_amd import _lib
@@ -230,7 +231,7 @@ class CpuLayer:
         self.pts = {k: [self.ctx.encode_to_ntt(p) for p in pack_rows(np.asarray(A[k], np.float64), N // 2)] for k in A}
         self.B = B
 
-    def run(self, layer, h, seed):
+    def run(self, layer, h, seed, rescale=True):
         from provenloop_amd.zero_moai import replicate
 
         cols = (N // 2) // D
@@ -239,7 +240,9 @@ class CpuLayer:
         for p in "qv":
             inter = np.zeros(RANK)
             for b, pt in enumerate(self.pts[(layer, p)]):
-                r = self.ctx.rescale(self.ctx.ct_pt_mul_ntt(ct, pt))
+                r = self.ctx.ct_pt_mul_ntt(ct, pt)
+                if rescale:
+                    r = self.ctx.rescale(r)
                 cts[(p, b)] = r
                 dec = self.ctx.decrypt(r, self.sk)
                 for i in range(min(cols, RANK - b * cols)):
@@ -693,13 +696,16 @@ def main():
     for w in range(args.warmup):
         dev.run(pk, sk, args.steps + w, warm_seeds[w])
     ctx.sync()
+    tok = []
     t0 = time.perf_counter()
     for t in range(args.steps):
         dev.run(pk, sk, t, seed_arr[t])
         ctx.sync()  # one host synchronisation per token
+        tok.append(time.perf_counter())
     elapsed = time.perf_counter() - t0
     deltas_per_token = LAYERS * 2
     value = deltas_per_token * args.steps / elapsed
+    tok_ms = np.diff(np.concatenate([[t0], tok])) * 1e3
 
     # the same tokens queued back to back (host launches overlap the GPU; one sync at the end)
     t2 = time.perf_counter()
@@ -714,20 +720,37 @@ def main():
         host_out = lora.deltas(pk, sk, np.stack(hidden[t]), seeds[t])
     pcie_elapsed = time.perf_counter() - t1
 
-    # parity on layers 0 and 27 of token steps-1 against the oracle
+    # the reference's own call sequence: ct x pt, then decrypt without a rescale
+    # (inference_engine.py:1311-1315; the CRT branch of ciphertext.rs:351-396)
+    t3 = time.perf_counter()
+    for t in range(args.steps):
+        dev.run(pk, sk, t, seed_arr[t], rescale=False)
+        ctx.sync()
+    norescale_elapsed = time.perf_counter() - t3
+    flat_nr = dev.deltas(args.steps - 1)
+
+    # parity on layers 0 and 27 of token steps-1 against the oracle (the
+    # device outputs of the rescaled pass were overwritten by the pass without
+    # rescale; the host-I/O pass left the same token's deltas in host_out)
     last = args.steps - 1
-    flat = dev.deltas(last)
-    dev_host_equal = bool(np.array_equal(flat, np.concatenate(host_out)))
+    flat = np.concatenate(host_out)
+    dev.run(pk, sk, last, seed_arr[last])
+    ctx.sync()
+    dev_host_equal = bool(np.array_equal(dev.deltas(last), flat))
     dev.free()
     cpu = CpuLayer(A, B)
     hs, sd = hidden[last], seeds[last]
-    rel = []
+    rel, rel_nr = [], []
     for l in (0, LAYERS - 1):
         ref, _, _ = cpu.run(l, hs[l], sd[l])
         for j, p in enumerate("qv"):
             k = 2 * l + j
             g, c = flat[lora.offsets[k]:lora.offsets[k + 1]], ref[p]
             rel.append(float(np.linalg.norm(g - c) / np.linalg.norm(c)))
+    ref_nr, _, _ = cpu.run(0, hs[0], sd[0], rescale=False)
+    for j, p in enumerate("qv"):
+        g, c = flat_nr[lora.offsets[j]:lora.offsets[j + 1]], ref_nr[p]
+        rel_nr.append(float(np.linalg.norm(g - c) / np.linalg.norm(c)))
     # bit-exact ciphertext check of one encrypt_pk + product + rescale
     from provenloop_amd import zero_moai
 
@@ -794,6 +817,16 @@ def main():
             "limiter": "neither HBM nor VALU saturated: per CU the loads, the 60-bit limbs' integer "
                        "arithmetic, the LDS exchanges and the stores follow one another (one polynomial "
                        "per CU at this batch); no MFMA work",
+        },
+        "token_ms": {"median": round(float(np.median(tok_ms)), 4), "first": round(float(tok_ms[0]), 4),
+                     "last": round(float(tok_ms[-1]), 4), "min": round(float(tok_ms.min()), 4)},
+        "reference_sequence": {
+            "value": round(deltas_per_token * args.steps / norescale_elapsed, 3), "unit": "deltas/s",
+            "ms_per_step": round(norescale_elapsed / args.steps * 1e3, 4),
+            "workload": "the same tokens through the reference's own call sequence (inference_engine.py:1311-1315): "
+                        "ct x pt, then decrypt without a rescale (scale 2^80: the CRT branch over limbs 0 and 1), "
+                        "segment sums, B @ intermediate; one host synchronisation per token",
+            "parity": {"delta_rel_err_max_layer0": max(rel_nr)},
         },
         "pipelined": {
             "value": round(deltas_per_token * args.steps / piped, 3), "unit": "deltas/s",

@@ -124,6 +124,23 @@ __global__ void k_sub_product(const uint64_t* __restrict__ x, const uint64_t* __
   }
 }
 
+// D = c0 + c1 s on limbs 0..nl-1 of count ciphertexts at cts + i ct_stride
+// ([c0 | c1], L limbs each), with the secret key in Montgomery form: the
+// decryption's c0 + c1 s (ciphertext.rs:332-341), lazily in [0, 3q). For a
+// product ciphertext (c0 pt, c1 pt) the decryption is pt (c0 + c1 s), so one
+// D per input serves every plaintext it is multiplied by.
+__global__ void k_key_dot(const uint64_t* __restrict__ cts, uint64_t ct_stride, const uint64_t* __restrict__ skm,
+                          uint64_t* __restrict__ out, const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L,
+                          uint32_t nl, uint64_t total) {
+  const uint64_t per = (uint64_t)nl * n;
+  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t i = e / per, r = e - i * per;
+    const uint32_t l = (uint32_t)(r / n);
+    const uint64_t* c = cts + i * ct_stride;
+    out[e] = c[r] + mont_mul(c[(uint64_t)L * n + r], skm[r], bc[l]);
+  }
+}
+
 // c0 = b*U + M, c1 = a*U + E1 in the NTT domain (ciphertext.rs:298-312).
 __global__ void k_encrypt_combine(const EncCombineJob* __restrict__ jobs, const BarrettConst* __restrict__ bc,
                                   uint32_t n, uint32_t L, const uint64_t* __restrict__ pk) {
@@ -189,6 +206,15 @@ hipError_t launch_to_montgomery(const uint64_t* src, uint64_t* dst, const Barret
   if (!total) return hipSuccess;
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
   hipLaunchKernelGGL(k_to_montgomery, dim3(blocks), dim3(256), 0, s, src, dst, bc, n, L, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_key_dot(const uint64_t* cts, uint64_t ct_stride, const uint64_t* skm, uint64_t* out,
+                          const BarrettConst* bc, uint32_t n, uint32_t L, uint32_t nl, uint32_t count, hipStream_t s) {
+  const uint64_t total = (uint64_t)count * nl * n;
+  if (!total) return hipSuccess;
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_key_dot, dim3(blocks), dim3(256), 0, s, cts, ct_stride, skm, out, bc, n, L, nl, total);
   return hipGetLastError();
 }
 

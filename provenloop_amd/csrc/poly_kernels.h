@@ -93,6 +93,9 @@ hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_lim
 hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, uint32_t k, uint32_t nb, uint32_t L,
                          uint32_t n, hipStream_t s);
 // pk (optional): the public key [b | a] for every job instead of the jobs' fields.
+// D = c0 + c1 s (lazy, [0, 3q)) on limbs 0..nl-1 of count ciphertexts, key in Montgomery form (k_key_dot).
+hipError_t launch_key_dot(const uint64_t* cts, uint64_t ct_stride, const uint64_t* skm, uint64_t* out,
+                          const BarrettConst* bc, uint32_t n, uint32_t L, uint32_t nl, uint32_t count, hipStream_t s);
 // count x L x n residues -> Montgomery form, w 2^64 mod q (k_to_montgomery).
 hipError_t launch_to_montgomery(const uint64_t* src, uint64_t* dst, const BarrettConst* bc, uint32_t n, uint32_t L,
                                 uint32_t count, hipStream_t s);

@@ -264,7 +264,7 @@ struct th_lora {
   int64_t* mvals = nullptr;    // n_in x N encoded messages m (i64)
   uint64_t* prep = nullptr;    // n_in x 3L x N
   uint64_t* cts = nullptr;     // n_in x 2L x N
-  uint64_t* work = nullptr;    // n_batches x 2L x N: rescale inverse transforms, or the products
+  uint64_t* work = nullptr;    // n_batches x 2L x N: the rescale's inverse transforms
   uint64_t* res = nullptr;     // n_batches x 2(L-1) x N
   uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
   double* sums = nullptr;      // n_batches x cols
@@ -272,13 +272,17 @@ struct th_lora {
   const SampleJob* d_sample = nullptr;
   const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
-  const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr, *d_dot_n = nullptr;
+  const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr;
   const NttJob* d_enc_ntt = nullptr;  // encrypt transforms: residues of m + e0, e1, u formed in the loads
   const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
+  // decrypt without a rescale: D = c0 + c1 s per input (k_key_dot), then per
+  // batch the inverse transforms of pt * D (the product's decryption)
+  uint64_t* dkey = nullptr;           // n_in x nl x N
+  const NttJob* d_inv_nr = nullptr;
+  uint32_t inv_nr_jobs = 0, nl_n = 1;
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
-  const CtPtJob* d_ctpt = nullptr;
   const LoraBJob* d_bjobs = nullptr;
-  uint32_t dot_n_jobs = 0, dot_r_jobs = 0;
+  uint32_t dot_r_jobs = 0;
   const double* seg_w = nullptr;  // segment weights, or null: decode the slots and sum them
   const double* seg_p = nullptr;  // the same in recurrence form (decrypt transform's epilogue)
   // gated (mixture) sets: k experts per projection, regated by th_lora_set_gates
@@ -2008,14 +2012,15 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     }
     set->d_enc_ntt = persist(set, ej2);
   }
-  std::vector<NttJob> inv, fwd, dot_r, dot_n;
+  std::vector<NttJob> inv, fwd, dot_r, inv_nr;
   std::vector<DecodeJob> dec_r(nb), dec_n(nb);
-  std::vector<CtPtJob> cp(nb);
   const uint32_t Lr = L > 1 ? L - 1 : 1;
   // decrypt branch (ciphertext.rs:351): CRT over limbs 0, 1 iff scale > 1.5 * 2^40 and >= 2 limbs
   const double scale_n = kScale * kScale, scale_r = scale_n / (double)c->q[L - 1];
   const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
+  set->nl_n = nl_n;
+  set->dkey = (uint64_t*)set->alloc((size_t)set->n_in * nl_n * P);
   for (uint32_t bt = 0; bt < nb; ++bt) {
     const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
     const uint64_t* pt = set->pts + (size_t)bt * L * N;
@@ -2036,9 +2041,10 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
       for (uint32_t l = 0; l < nl_r; ++l)
         dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(Lr + l) * N, nullptr, l, 0});
     }
-    for (uint32_t l = 0; l < nl_n; ++l)
-      dot_n.push_back(NttJob{w + (size_t)l * N, mm + (size_t)l * N, w + (size_t)(L + l) * N, nullptr, l, 0});
-    cp[bt] = CtPtJob{ct, ct + (size_t)L * N, pt, w, L, 0};
+    for (uint32_t l = 0; l < nl_n; ++l) {
+      inv_nr.push_back(NttJob{set->dkey + ((size_t)batch_input[bt] * nl_n + l) * N, mm + (size_t)l * N,
+                              ptm + (size_t)l * N, nullptr, l, 0});
+    }
     dec_r[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
                           scale_r, nl_r == 2, 0};
     dec_n[bt] = DecodeJob{mm, dec_parts + bt * decode_parts_doubles(c->logn), nullptr, set->sums + (size_t)bt * cols,
@@ -2059,11 +2065,10 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
       set->d_dot_seg = persist(set, ds);
     }
   }
-  set->d_dot_n = persist(set, dot_n);
-  set->dot_n_jobs = (uint32_t)dot_n.size();
+  set->d_inv_nr = persist(set, inv_nr);
+  set->inv_nr_jobs = (uint32_t)inv_nr.size();
   set->dot_r_jobs = (uint32_t)dot_r.size();
   set->d_dec_n = persist(set, dec_n);
-  set->d_ctpt = persist(set, cp);
   set->d_bjobs = persist(set, bj);
   if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
   if (set->d_dot_seg) set->seg_p = seg_pairs(c, d);
@@ -2123,8 +2128,11 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
     if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
   } else {
-    HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
-    launch_jobs_ntt(ctx, true, set->d_dot_n, set->dot_n_jobs, NTT_LOAD_DOT, nullptr, sk->d);
+    // the product ciphertexts (c0 pt, c1 pt) decrypt to pt (c0 + c1 s): D once
+    // per input, then each batch's inverse transforms with pt * D in their loads
+    HIPCHK(launch_key_dot(set->cts, (uint64_t)2 * L * N, sk_montgomery(ctx, sk), set->dkey, ctx->d_bc, N, L,
+                          set->nl_n, ni, st));
+    launch_jobs_ntt(ctx, true, set->d_inv_nr, set->inv_nr_jobs, NTT_LOAD_MULM);
   }
   const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
   if (do_rescale && set->d_dot_seg)
