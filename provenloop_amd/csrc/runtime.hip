@@ -265,7 +265,7 @@ struct th_lora {
   uint64_t* prep = nullptr;    // n_in x 3L x N
   uint64_t* cts = nullptr;     // n_in x 2L x N
   uint64_t* work = nullptr;    // n_batches x 2L x N: the rescale's inverse transforms
-  uint64_t* res = nullptr;     // n_batches x 2(L-1) x N
+  uint64_t* res = nullptr;     // n_batches x 2 nl_r x N: the rescaled limbs the decryption reads
   uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
   double* sums = nullptr;      // n_batches x cols
   double* deltas = nullptr;    // n_deltas
@@ -280,6 +280,7 @@ struct th_lora {
   uint64_t* dkey = nullptr;           // n_in x nl x N
   const NttJob* d_inv_nr = nullptr;
   uint32_t inv_nr_jobs = 0, nl_n = 1;
+  uint32_t nl_r = 1;  // limbs a rescaled product's decryption reads (1, or 2 for the CRT branch)
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
   const LoraBJob* d_bjobs = nullptr;
   uint32_t dot_r_jobs = 0;
@@ -1951,7 +1952,6 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   double* enc_parts = (double*)set->alloc(ni * encode_parts_doubles(c->logn) * 8);
   set->cts = (uint64_t*)set->alloc(ni * 2 * L * P);
   set->work = (uint64_t*)set->alloc(nb * 2 * L * P);
-  set->res = (uint64_t*)set->alloc(nb * 2 * (L > 1 ? L - 1 : 1) * P);
   set->m = (uint64_t*)set->alloc(nb * 2 * P);
   double* dec_parts = (double*)set->alloc(nb * decode_parts_doubles(c->logn) * 8);
   set->sums = (double*)set->alloc((size_t)nb * cols * 8);
@@ -2020,26 +2020,32 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
   set->nl_n = nl_n;
+  set->nl_r = nl_r;
+  set->res = (uint64_t*)set->alloc(nb * 2 * nl_r * P);
   set->dkey = (uint64_t*)set->alloc((size_t)set->n_in * nl_n * P);
   for (uint32_t bt = 0; bt < nb; ++bt) {
     const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
     const uint64_t* pt = set->pts + (size_t)bt * L * N;
     const uint64_t* ptm = set->ptm + (size_t)bt * L * N;
     uint64_t* w = set->work + (size_t)bt * 2 * L * N;
-    uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
+    uint64_t* r = set->res + (size_t)bt * 2 * nl_r * N;
     uint64_t* mm = set->m + (size_t)bt * 2 * N;
     if (L >= 2) {
       // evaluation-domain rescale of ct x pt (see queue_rescale): inverse NTT of the product's
-      // last limb (into the batch's work area), forward NTTs of it reduced to each other limb
+      // last limb (into the batch's work area), forward NTTs of it reduced to the limbs the
+      // decryption reads. Limb l of the rescaled ciphertext depends on limbs l and L-1 of the
+      // product only, and the decryption reads limb 0 (limbs 0 and 1 in the CRT branch,
+      // ciphertext.rs:351-353, encoding.rs:221-226), so the other limbs are not formed; their
+      // residues would be those of th_rescale.
       for (uint32_t comp = 0; comp < 2; ++comp) {
         const uint64_t* cc = ct + (size_t)comp * L * N;
         uint64_t* lc = w + (size_t)comp * N;
         inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, ptm + (size_t)(L - 1) * N, nullptr, L - 1, 0});
-        for (uint32_t l = 0; l + 1 < L; ++l)
-          fwd.push_back(NttJob{lc, r + (size_t)(comp * Lr + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
+        for (uint32_t l = 0; l < nl_r; ++l)
+          fwd.push_back(NttJob{lc, r + (size_t)(comp * nl_r + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
       }
       for (uint32_t l = 0; l < nl_r; ++l)
-        dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(Lr + l) * N, nullptr, l, 0});
+        dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(nl_r + l) * N, nullptr, l, 0});
     }
     for (uint32_t l = 0; l < nl_n; ++l) {
       inv_nr.push_back(NttJob{set->dkey + ((size_t)batch_input[bt] * nl_n + l) * N, mm + (size_t)l * N,
@@ -2058,9 +2064,8 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     if (nl_r == 1 && segsum_in_transform(c, nb, cols)) {
       std::vector<NttJob> ds(nb);
       for (uint32_t bt = 0; bt < nb; ++bt) {
-        const uint64_t* r = set->res + (size_t)bt * 2 * Lr * N;
-        ds[bt] = NttJob{r, reinterpret_cast<uint64_t*>(set->sums + (size_t)bt * cols), r + (size_t)Lr * N, nullptr, 0, 0,
-                        scale_r};
+        const uint64_t* r = set->res + (size_t)bt * 2 * N;
+        ds[bt] = NttJob{r, reinterpret_cast<uint64_t*>(set->sums + (size_t)bt * cols), r + N, nullptr, 0, 0, scale_r};
       }
       set->d_dot_seg = persist(set, ds);
     }
@@ -2125,7 +2130,7 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     fa.load = NTT_LOAD_REDUCE;
     fa.store = NTT_STORE_MUL_RESCALE;
     fa.rc = ctx->d_rc + (size_t)L * L;
-    HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
+    HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * set->nl_r, st));
     if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
   } else {
     // the product ciphertexts (c0 pt, c1 pt) decrypt to pt (c0 + c1 s): D once
