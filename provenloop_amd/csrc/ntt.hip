@@ -216,6 +216,80 @@ __device__ __forceinline__ void inv_passes(typename A::V (&x)[Shape<LOGN>::E], t
   }
 }
 
+// Segment-sum epilogue of an inverse transform on limb 0 (NTT_STORE_SEGSUM):
+// the thread's canonical coefficients m (element k at j = elem(tid, k) of
+// layout END) are centred against q / 2 and accumulated as v_j W_c[j] for
+// every segment c; a fixed shuffle tree sums each wavefront and the
+// wavefronts' sums are added in order, so the result does not depend on
+// scheduling. RESCALED: m is first taken to (m - (xl[j] mod q)) * inv mod q
+// with the rescale constants *rc (the coefficient-domain end of a rescaled
+// decryption, rescale_decrypt_kernel).
+template <int LOGN, int END, bool RESCALED, class A>
+__device__ __forceinline__ void segsum_store(const typename A::V (&x)[Shape<LOGN>::E], const A& ar, uint64_t q,
+                                             uint32_t tid, const double* segw, uint32_t cols, double* seg,
+                                             double scale, const uint64_t* xl, const RescaleConst* rcp,
+                                             void* lds_raw) {
+  using S = Shape<LOGN>;
+  constexpr int MAXC = NTT_SEGSUM_FUSED_MAX_COLS;
+  const uint64_t half = q >> 1;
+  using D2 = double __attribute__((ext_vector_type(2)));
+  const GPtr<D2> W = gld(reinterpret_cast<const D2*>(segw));
+  double acc[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
+  // the weights (and subtrahends) of element k + PF are requested while
+  // element k is summed
+  constexpr int PF = S::E < 4 ? S::E : 4;
+  D2 wq[PF];
+  uint64_t xq[PF];
+  RescaleConst rc{};
+  if constexpr (RESCALED) rc = *rcp;
+  __builtin_amdgcn_sched_barrier(0);  // keep the requests after the last pass (register peak)
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    wq[k] = W[elem<S::LE, END>(tid, k)];
+    if constexpr (RESCALED) xq[k] = gld(xl)[elem<S::LE, END>(tid, k)];
+  }
+#pragma unroll
+  for (int k = 0; k < S::E; ++k) {
+    uint64_t m = ar.inv_store(x[k]);
+    if constexpr (RESCALED) {
+      const uint64_t xv = xq[k % PF];
+      if (k + PF < S::E) xq[k % PF] = gld(xl)[elem<S::LE, END>(tid, k + PF)];
+      const uint64_t xr = xv < rc.q ? xv : mulmod_barrett(xv, 1, rc.b);
+      m = csub(shoup_lazy(submod(m, xr, q), rc.inv, rc.inv_s, q), q);
+    }
+    const double v = m > half ? -(double)(q - m) : (double)m;
+    const D2 p = wq[k % PF];  // W_0[j], 2 cos(2 phi_j) at j = elem(tid, k)
+    if (k + PF < S::E) wq[k % PF] = W[elem<S::LE, END>(tid, k + PF)];
+    double wp = p.x, wc = p.x;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      if (c >= (int)cols) break;
+      acc[c] += v * wc;
+      const double wn = p.y * wc - wp;
+      wp = wc;
+      wc = wn;
+    }
+  }
+  double* red = reinterpret_cast<double*>(lds_raw);
+  const uint32_t lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    if (c >= (int)cols) break;
+    double a = acc[c];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
+    if (lane == 0) red[wave * MAXC + c] = a;
+  }
+  __syncthreads();
+  if (tid < cols) {
+    double t = 0.0;
+    for (uint32_t w = 0; w < S::T / 64; ++w) t += red[w * MAXC + tid];
+    gst(seg)[tid] = t / scale;
+  }
+}
+
 template <int LOGN, bool INV, class A, class LOp, class SOp>
 __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
                                         const LimbConst& lc, const LOp& op, const SOp& so, void* lds_raw) {
@@ -242,54 +316,7 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
     inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, tw, ar, lc);
     constexpr int END = inv_end_lo<LOGN>();
     if constexpr (SOp::kind == NTT_STORE_SEGSUM) {
-      // segment sums of the centred coefficients (limb 0): per-thread partial
-      // sums, a fixed butterfly tree per wavefront, then the wavefronts' sums
-      // in order, so the result does not depend on scheduling
-      constexpr int MAXC = NTT_SEGSUM_FUSED_MAX_COLS;
-      const uint64_t q = lc.q, half = q >> 1;
-      using D2 = double __attribute__((ext_vector_type(2)));
-      const GPtr<D2> W = gld(reinterpret_cast<const D2*>(so.segw));
-      double acc[MAXC];
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
-      // the weights of element k + PF are requested while element k is summed
-      constexpr int PF = S::E < 4 ? S::E : 4;
-      D2 wq[PF];
-      __builtin_amdgcn_sched_barrier(0);  // keep the requests after the last pass (register peak)
-#pragma unroll
-      for (int k = 0; k < PF; ++k) wq[k] = W[elem<S::LE, END>(tid, k)];
-#pragma unroll
-      for (int k = 0; k < S::E; ++k) {
-        const uint64_t m = ar.inv_store(x[k]);
-        const double v = m > half ? -(double)(q - m) : (double)m;
-        const D2 p = wq[k % PF];  // W_0[j], 2 cos(2 phi_j) at j = elem(tid, k)
-        if (k + PF < S::E) wq[k % PF] = W[elem<S::LE, END>(tid, k + PF)];
-        double wp = p.x, wc = p.x;
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c) {
-          if (c >= (int)so.cols) break;
-          acc[c] += v * wc;
-          const double wn = p.y * wc - wp;
-          wp = wc;
-          wc = wn;
-        }
-      }
-      double* red = reinterpret_cast<double*>(lds_raw);
-      const uint32_t lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        if (c >= (int)so.cols) break;
-        double a = acc[c];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
-        if (lane == 0) red[wave * MAXC + c] = a;
-      }
-      __syncthreads();
-      if (tid < so.cols) {
-        double t = 0.0;
-        for (uint32_t w = 0; w < S::T / 64; ++w) t += red[w * MAXC + tid];
-        gst(so.seg)[tid] = t / so.scale;
-      }
+      segsum_store<LOGN, END, false>(x, ar, lc.q, tid, so.segw, so.cols, so.seg, so.scale, nullptr, nullptr, lds_raw);
     } else {
 #pragma unroll
       for (int k = 0; k < S::E; ++k) gdst[elem<S::LE, END>(tid, k)] = ar.inv_store(x[k]);
@@ -322,6 +349,94 @@ __global__ __launch_bounds__(Shape<LOGN>::T) void ntt_kernel(NttArgs a) {
     run_ntt<LOGN, INV, Fp64Arith>(src, dst, lc, op, so, lds);
   else
     run_ntt<LOGN, INV, IntArith>(src, dst, lc, op, so, lds);
+}
+
+// One rescaled product's decryption on limb 0, with its segment sums
+// (RescaleDecryptJob). The rescale (ciphertext.rs:476-535) takes each
+// component c_i of ct x pt to (c_i - NTT(r_i)) inv on limb 0, where r_i is the
+// last limb's coefficients reduced mod q and inv = q_last^{-1} mod q, and the
+// decryption (ciphertext.rs:327-346) forms c'_0 + c'_1 s and transforms it
+// back. With c_i = ct_i pt and D = ct_0 + ct_1 s, and the NTT linear mod q,
+//   INTT(c'_0 + c'_1 s) = (INTT(D pt - NTT(r_1) s) - r_0) inv  (mod q),
+// the same residues. So one workgroup runs the forward transform of r_1 (the
+// loads reduce the last limb's coefficients Y mod q), forms D pt - NTT(r_1) s
+// in registers at the forward's output positions (the inverse's input
+// positions), runs the inverse transform, and subtracts r_0 (from X) and
+// scales in the segment-sum epilogue. Two transforms per product, where the
+// rescaled ciphertext and its decryption take three, and nothing but the
+// segment sums is written.
+template <int LOGN, class A>
+__device__ __forceinline__ void run_rescale_decrypt(const RescaleDecryptArgs& a, const RescaleDecryptJob& jb,
+                                                    const LimbConst& lc, void* lds_raw) {
+  using S = Shape<LOGN>;
+  const uint32_t tid = threadIdx.x;
+  const A ar(lc);
+  const RescaleConst* rcp = a.rc;
+  const BarrettConst bc = *a.bc;
+  typename A::V x[S::E];
+  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  {
+    const GPtr<uint64_t> y = gld(jb.y);
+    const uint64_t q = rcp->q;
+#pragma unroll
+    for (int k = 0; k < S::E; ++k) {
+      const uint64_t v = y[elem<S::LE, S::COAL_LO>(tid, k)];
+      x[k] = ar.load(v < q ? v : mulmod_barrett(v, 1, rcp->b));
+    }
+  }
+  fwd_passes<LOGN, LOGN, S::COAL_LO, A>(x, lds, tid, gld(reinterpret_cast<const typename A::Tw*>(lc.fwd)), ar);
+  {
+    // D pt - NTT(r_1) s: Montgomery products with pt and s in Montgomery
+    // form, each in [0, 2q), so the difference plus 2q is in (0, 4q): the
+    // integer inverse's input range; the FP64 inverse gets it canonical
+    const GPtr<uint64_t> d = gld(jb.d), p = gld(jb.ptm), sk = gld(a.skm);
+    const uint64_t q = lc.q, two_q = 2 * lc.q;
+#pragma unroll
+    for (int k = 0; k < S::E; ++k) {
+      const uint32_t i = elem<S::LE, S::WAVE_LO>(tid, k);
+      const uint64_t u = mont_mul(d[i], p[i], bc);
+      const uint64_t t = mont_mul(ar.fwd_store(x[k]), sk[i], bc);
+      uint64_t e = u + two_q - t;
+      if constexpr (std::is_same_v<A, Fp64Arith>) e = csub(csub(e, two_q), q);
+      x[k] = ar.load(e);
+    }
+  }
+  inv_passes<LOGN, 0, S::WAVE_LO, A>(x, lds, tid, gld(reinterpret_cast<const typename A::Tw*>(lc.inv)), ar, lc);
+  segsum_store<LOGN, inv_end_lo<LOGN>(), true>(x, ar, lc.q, tid, a.segw, a.cols, jb.seg, jb.scale, jb.x, rcp,
+                                               lds_raw);
+}
+
+template <int LOGN>
+__global__ __launch_bounds__(Shape<LOGN>::T) void rescale_decrypt_kernel(RescaleDecryptArgs a) {
+  extern __shared__ uint64_t lds[];
+  const RescaleDecryptJob jb = a.jobs[blockIdx.x];
+  const LimbConst& lc = a.lc[0];
+  if (lc.fp64)
+    run_rescale_decrypt<LOGN, Fp64Arith>(a, jb, lc, lds);
+  else
+    run_rescale_decrypt<LOGN, IntArith>(a, jb, lc, lds);
+}
+
+template <int LOGN>
+static hipError_t launch_rescale_decrypt_t(const RescaleDecryptArgs& a, uint32_t njobs, hipStream_t s) {
+  const hipError_t e = allow_full_lds<rescale_decrypt_kernel<LOGN>>();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((rescale_decrypt_kernel<LOGN>), dim3(njobs), dim3(Shape<LOGN>::T),
+                     (size_t)Shape<LOGN>::LDS_ELEMS * 8, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rescale_decrypt(int logn, const RescaleDecryptArgs& a, uint32_t njobs, hipStream_t s) {
+  if (njobs == 0) return hipSuccess;
+  if (a.cols < 1 || a.cols > NTT_SEGSUM_FUSED_MAX_COLS) return hipErrorInvalidValue;
+  switch (logn) {
+    case 10: return launch_rescale_decrypt_t<10>(a, njobs, s);
+    case 11: return launch_rescale_decrypt_t<11>(a, njobs, s);
+    case 12: return launch_rescale_decrypt_t<12>(a, njobs, s);
+    case 13: return launch_rescale_decrypt_t<13>(a, njobs, s);
+    case 14: return launch_rescale_decrypt_t<14>(a, njobs, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int LOGN, bool INV>

@@ -275,6 +275,9 @@ struct th_lora {
   const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr;
   const NttJob* d_enc_ntt = nullptr;  // encrypt transforms: residues of m + e0, e1, u formed in the loads
   const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
+  // rescaled products decrypted on limb 0 straight from the last limb's
+  // inverse transforms (rescale_decrypt_kernel), one job per batch
+  const RescaleDecryptJob* d_rd = nullptr;
   // decrypt without a rescale: D = c0 + c1 s per input (k_key_dot), then per
   // batch the inverse transforms of pt * D (the product's decryption)
   uint64_t* dkey = nullptr;           // n_in x nl x N
@@ -2013,6 +2016,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->d_enc_ntt = persist(set, ej2);
   }
   std::vector<NttJob> inv, fwd, dot_r, inv_nr;
+  std::vector<RescaleDecryptJob> rd;
   std::vector<DecodeJob> dec_r(nb), dec_n(nb);
   const uint32_t Lr = L > 1 ? L - 1 : 1;
   // decrypt branch (ciphertext.rs:351): CRT over limbs 0, 1 iff scale > 1.5 * 2^40 and >= 2 limbs
@@ -2021,14 +2025,17 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
   set->nl_n = nl_n;
   set->nl_r = nl_r;
-  set->res = (uint64_t*)set->alloc(nb * 2 * nl_r * P);
+  // rescaled products straight into segment sums (rescale_decrypt_kernel)
+  // where the decryption reads limb 0 and its transform can sum the segments
+  const bool fused_rd = L >= 2 && nl_r == 1 && segsum_in_transform(c, nb, cols);
+  if (!fused_rd) set->res = (uint64_t*)set->alloc(nb * 2 * nl_r * P);
   set->dkey = (uint64_t*)set->alloc((size_t)set->n_in * nl_n * P);
   for (uint32_t bt = 0; bt < nb; ++bt) {
     const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
     const uint64_t* pt = set->pts + (size_t)bt * L * N;
     const uint64_t* ptm = set->ptm + (size_t)bt * L * N;
     uint64_t* w = set->work + (size_t)bt * 2 * L * N;
-    uint64_t* r = set->res + (size_t)bt * 2 * nl_r * N;
+    uint64_t* r = fused_rd ? nullptr : set->res + (size_t)bt * 2 * nl_r * N;
     uint64_t* mm = set->m + (size_t)bt * 2 * N;
     if (L >= 2) {
       // evaluation-domain rescale of ct x pt (see queue_rescale): inverse NTT of the product's
@@ -2041,11 +2048,17 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
         const uint64_t* cc = ct + (size_t)comp * L * N;
         uint64_t* lc = w + (size_t)comp * N;
         inv.push_back(NttJob{cc + (size_t)(L - 1) * N, lc, ptm + (size_t)(L - 1) * N, nullptr, L - 1, 0});
-        for (uint32_t l = 0; l < nl_r; ++l)
-          fwd.push_back(NttJob{lc, r + (size_t)(comp * nl_r + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
+        if (!fused_rd)
+          for (uint32_t l = 0; l < nl_r; ++l)
+            fwd.push_back(
+                NttJob{lc, r + (size_t)(comp * nl_r + l) * N, cc + (size_t)l * N, pt + (size_t)l * N, l, 0});
       }
-      for (uint32_t l = 0; l < nl_r; ++l)
-        dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(nl_r + l) * N, nullptr, l, 0});
+      if (fused_rd)
+        rd.push_back(RescaleDecryptJob{w + N, w, set->dkey + (size_t)batch_input[bt] * N, ptm,
+                                       set->sums + (size_t)bt * cols, scale_r});
+      else
+        for (uint32_t l = 0; l < nl_r; ++l)
+          dot_r.push_back(NttJob{r + (size_t)l * N, mm + (size_t)l * N, r + (size_t)(nl_r + l) * N, nullptr, l, 0});
     }
     for (uint32_t l = 0; l < nl_n; ++l) {
       inv_nr.push_back(NttJob{set->dkey + ((size_t)batch_input[bt] * nl_n + l) * N, mm + (size_t)l * N,
@@ -2058,9 +2071,13 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   }
   if (L >= 2) {
     set->d_inv_mul = persist(set, inv);
+    set->d_dec_r = persist(set, dec_r);
+  }
+  if (fused_rd) {
+    set->d_rd = persist(set, rd);
+  } else if (L >= 2) {
     set->d_fwd_rs = persist(set, fwd);
     set->d_dot_r = persist(set, dot_r);
-    set->d_dec_r = persist(set, dec_r);
     if (nl_r == 1 && segsum_in_transform(c, nb, cols)) {
       std::vector<NttJob> ds(nb);
       for (uint32_t bt = 0; bt < nb; ++bt) {
@@ -2076,7 +2093,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->d_dec_n = persist(set, dec_n);
   set->d_bjobs = persist(set, bj);
   if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
-  if (set->d_dot_seg) set->seg_p = seg_pairs(c, d);
+  if (set->d_dot_seg || set->d_rd) set->seg_p = seg_pairs(c, d);
   HIPCHK(hipStreamSynchronize(c->stream));
 }
 
@@ -2119,7 +2136,23 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk_pairs(ctx, pk), set->cts, &combined, st));
     if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
   }
-  if (do_rescale) {
+  if (do_rescale && set->d_rd) {
+    // the last limb of (c0 pt, c1 pt) as coefficients (ct x pt in the inverse
+    // transforms' loads), D = c0 + c1 s on limb 0 per input, then each batch's
+    // rescale and decryption on limb 0 in one kernel, which writes the sums
+    launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MULM);
+    const uint64_t* skm = sk_montgomery(ctx, sk);
+    HIPCHK(launch_key_dot(set->cts, (uint64_t)2 * L * N, skm, set->dkey, ctx->d_bc, N, L, 1, ni, st));
+    RescaleDecryptArgs ra{};
+    ra.lc = ctx->d_lc;
+    ra.bc = ctx->d_bc;
+    ra.rc = ctx->d_rc + (size_t)L * L;
+    ra.skm = skm;
+    ra.segw = set->seg_p;
+    ra.jobs = set->d_rd;
+    ra.cols = set->cols;
+    HIPCHK(launch_rescale_decrypt((int)ctx->logn, ra, nb, st));
+  } else if (do_rescale) {
     // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
     NttArgs ia{}, fa{};
     ia.lc = fa.lc = ctx->d_lc;
@@ -2140,7 +2173,9 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     launch_jobs_ntt(ctx, true, set->d_inv_nr, set->inv_nr_jobs, NTT_LOAD_MULM);
   }
   const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;
-  if (do_rescale && set->d_dot_seg)
+  if (do_rescale && set->d_rd) {
+    // the sums are written
+  } else if (do_rescale && set->d_dot_seg)
     launch_dot_segsum(ctx, set->d_dot_seg, nb, sk, set->seg_p, set->cols);
   else if (set->seg_w)
     HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));

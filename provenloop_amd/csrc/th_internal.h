@@ -82,6 +82,28 @@ struct NttArgs {
   uint32_t pad_;
 };
 
+// One product ct x pt of a LoRA set, rescaled and decrypted on limb 0 into
+// its segment sums (rescale_decrypt_kernel): X, Y = the last limb of c0 pt
+// and c1 pt as coefficients (inverse transforms, canonical mod q_last).
+struct RescaleDecryptJob {
+  const uint64_t* y;
+  const uint64_t* x;
+  const uint64_t* d;    // c0 + c1 s of the product's input on limb 0, in [0, 3q) (k_key_dot)
+  const uint64_t* ptm;  // the plaintext's limb 0 in Montgomery form
+  double* seg;          // cols segment sums
+  double scale;         // the rescaled ciphertext's scale
+};
+struct RescaleDecryptArgs {
+  const LimbConst* lc;          // limb 0 is lc[0]
+  const BarrettConst* bc;       // limb 0
+  const RescaleConst* rc;       // limb 0 at the products' level
+  const uint64_t* skm;          // the secret key's limb 0 in Montgomery form
+  const double* segw;           // segment weight pairs, N x 2 (NTT_STORE_SEGSUM)
+  const RescaleDecryptJob* jobs;
+  uint32_t cols;                // segments per job, at most NTT_SEGSUM_FUSED_MAX_COLS
+  uint32_t pad_;
+};
+
 // Lets kernel K use up to the whole 160 KiB of a CU's LDS as dynamic shared
 // memory. Set once per kernel (the first call's result is kept), so launches
 // on the per-token path do not repeat the driver call.
@@ -110,6 +132,8 @@ hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t
 // are one kernel (the last limb's coefficients stay in registers).
 hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nfwd,
                           hipStream_t s);
+// njobs rescale_decrypt_kernel workgroups (whole-polynomial sizes, N <= 16384).
+hipError_t launch_rescale_decrypt(int logn, const RescaleDecryptArgs& a, uint32_t njobs, hipStream_t s);
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;
