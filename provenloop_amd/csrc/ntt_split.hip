@@ -474,18 +474,24 @@ hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, con
 // w % PARTS of input / limb w / PARTS with three wavefronts, one per
 // transform (0: M, 1: U, 2: E1), each with its own LDS slice; U's wavefront
 // hands its canonical outputs to the other two through LDS, which form and
-// store c0 and c1. jobs: 3L per input (M_0..M_{L-1}, E1_0.., U_0..);
+// store c0 and c1. The limbs are those in mask (n of them); jobs: 3n per
+// input (M, E1 and U of each of those limbs in increasing order);
 // pkp = [b (L) | a (L)] as prepared pairs (w, companion), so each product is
 // one Shoup or FP64 step; input i's ciphertext at cts + i 2 L N.
 template <int LOGN>
-__global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pkp, uint64_t* cts, uint32_t L) {
+__global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pkp, uint64_t* cts, uint32_t L,
+                                                          uint32_t mask) {
   using S = Split<LOGN>;
   __shared__ uint64_t lds[3][S::LDS];
+  const uint32_t nl = (uint32_t)__builtin_popcount(mask);
   const uint32_t part = blockIdx.x % S::PARTS, il = blockIdx.x / S::PARTS;
-  const uint32_t i = il / L, l = il % L;
+  const uint32_t i = il / nl, kl = il % nl;
+  uint32_t rest = mask;  // the kl-th set bit of mask is the limb
+  for (uint32_t j = 0; j < kl; ++j) rest &= rest - 1;
+  const uint32_t l = (uint32_t)__builtin_ctz(rest);
   const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const NttJob* jb = a.jobs + (size_t)i * 3 * L;
-  const uint32_t job = wv == 0 ? l : (wv == 1 ? 2 * L + l : L + l);
+  const NttJob* jb = a.jobs + (size_t)i * 3 * nl;
+  const uint32_t job = wv == 0 ? kl : (wv == 1 ? 2 * nl + kl : nl + kl);
   const LimbConst& lc = a.lc[l];
   const BarrettConst bc = a.bc[l];
   const size_t off = (size_t)l * S::N + ((size_t)part << 10) + lane;
@@ -535,21 +541,23 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
 }
 
 template <int LOGN>
-static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp, uint64_t* cts,
-                                   hipStream_t s) {
+static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t mask, const uint64_t* pkp,
+                                   uint64_t* cts, hipStream_t s) {
   using S = Split<LOGN>;
+  const uint32_t nl = (uint32_t)__builtin_popcount(mask);
   hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, NTT_LOAD_ENC, NTT_STORE_NONE>),
-                     dim3(ninputs * 3 * L * S::PARTS), dim3(64), 0, s, a);
-  hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * L * S::PARTS), dim3(192), 0, s, a, pkp, cts, L);
+                     dim3(ninputs * 3 * nl * S::PARTS), dim3(64), 0, s, a);
+  hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * nl * S::PARTS), dim3(192), 0, s, a, pkp, cts, L,
+                     mask);
   return hipGetLastError();
 }
 
-hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
-                                uint64_t* cts, hipStream_t s) {
+hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
+                                const uint64_t* pkp, uint64_t* cts, hipStream_t s) {
   switch (logn) {
-    case 13: return launch_encrypt_t<13>(a, ninputs, L, pkp, cts, s);
-    case 14: return launch_encrypt_t<14>(a, ninputs, L, pkp, cts, s);
-    case 15: return launch_encrypt_t<15>(a, ninputs, L, pkp, cts, s);
+    case 13: return launch_encrypt_t<13>(a, ninputs, L, limb_mask, pkp, cts, s);
+    case 14: return launch_encrypt_t<14>(a, ninputs, L, limb_mask, pkp, cts, s);
+    case 15: return launch_encrypt_t<15>(a, ninputs, L, limb_mask, pkp, cts, s);
     default: return hipErrorInvalidValue;
   }
 }

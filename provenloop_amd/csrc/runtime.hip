@@ -20,8 +20,10 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <tuple>
 #include <unordered_map>
 #include <unordered_set>
+#include <utility>
 #include <vector>
 
 #include "encode_sample.h"
@@ -273,7 +275,10 @@ struct th_lora {
   const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
   const NttJob *d_inv_mul = nullptr, *d_fwd_rs = nullptr, *d_dot_r = nullptr;
-  const NttJob* d_enc_ntt = nullptr;  // encrypt transforms: residues of m + e0, e1, u formed in the loads
+  // encrypt transforms (residues of m + e0, e1, u formed in the loads) of the
+  // limbs a token with (r) or without (n) a rescale reads, and those limbs
+  const NttJob *d_enc_r = nullptr, *d_enc_n = nullptr;
+  uint32_t enc_mask_r = 0, enc_mask_n = 0;
   const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
   // rescaled products decrypted on limb 0 straight from the last limb's
   // inverse transforms (rescale_decrypt_kernel), one job per batch
@@ -1999,22 +2004,6 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     ej[i].parts = enc_parts + i * encode_parts_doubles(c->logn);
   }
   set->d_enc = persist(set, ej);
-  {
-    // the encrypt inputs' forward transforms read m, e0, e1 and u and form
-    // each limb's residues as they load them: [M_l = m + e0 | E1_l | U_l] per input
-    std::vector<NttJob> ej2;
-    for (uint32_t i = 0; i < ni; ++i) {
-      uint64_t* pr = set->prep + (size_t)i * 3 * L * N;
-      const uint64_t* m = reinterpret_cast<const uint64_t*>(set->mvals + (size_t)i * N);
-      const uint64_t* e0 = reinterpret_cast<const uint64_t*>(set->e0 + (size_t)i * N);
-      const uint64_t* e1 = reinterpret_cast<const uint64_t*>(set->e1 + (size_t)i * N);
-      const uint64_t* u = reinterpret_cast<const uint64_t*>(set->u + (size_t)i * N);
-      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{m, pr + (size_t)l * N, e0, nullptr, l, 0});
-      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{e1, pr + (size_t)(L + l) * N, nullptr, nullptr, l, 1});
-      for (uint32_t l = 0; l < L; ++l) ej2.push_back(NttJob{u, pr + (size_t)(2 * L + l) * N, nullptr, nullptr, l, 2});
-    }
-    set->d_enc_ntt = persist(set, ej2);
-  }
   std::vector<NttJob> inv, fwd, dot_r, inv_nr;
   std::vector<RescaleDecryptJob> rd;
   std::vector<DecodeJob> dec_r(nb), dec_n(nb);
@@ -2025,6 +2014,44 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
   set->nl_n = nl_n;
   set->nl_r = nl_r;
+  {
+    // the encrypt inputs' forward transforms read m, e0, e1 and u and form
+    // each limb's residues as they load them: [M_l = m + e0 | E1_l | U_l] per
+    // input, for the limbs in mask
+    auto enc_jobs = [&](uint32_t mask) {
+      std::vector<NttJob> ej2;
+      for (uint32_t i = 0; i < ni; ++i) {
+        uint64_t* pr = set->prep + (size_t)i * 3 * L * N;
+        const uint64_t* m = reinterpret_cast<const uint64_t*>(set->mvals + (size_t)i * N);
+        const uint64_t* e0 = reinterpret_cast<const uint64_t*>(set->e0 + (size_t)i * N);
+        const uint64_t* e1 = reinterpret_cast<const uint64_t*>(set->e1 + (size_t)i * N);
+        const uint64_t* u = reinterpret_cast<const uint64_t*>(set->u + (size_t)i * N);
+        for (uint32_t l = 0; l < L; ++l)
+          if (mask >> l & 1) ej2.push_back(NttJob{m, pr + (size_t)l * N, e0, nullptr, l, 0});
+        for (uint32_t l = 0; l < L; ++l)
+          if (mask >> l & 1) ej2.push_back(NttJob{e1, pr + (size_t)(L + l) * N, nullptr, nullptr, l, 1});
+        for (uint32_t l = 0; l < L; ++l)
+          if (mask >> l & 1) ej2.push_back(NttJob{u, pr + (size_t)(2 * L + l) * N, nullptr, nullptr, l, 2});
+      }
+      return ej2;
+    };
+    // A token reads only some limbs of its input ciphertexts: the decryption
+    // reads limb 0 (limbs 0 and 1 in the CRT branch) of what it decrypts, a
+    // product's limb l depends on the input's limb l only, and a rescaled
+    // limb l on limbs l and L-1. So a token with a rescale needs limbs
+    // 0..nl_r-1 and L-1 of each input, one without a rescale limbs 0..nl_n-1;
+    // the encryptions form only those limbs where the transform size allows
+    // it (the other limbs would be the same residues as th_encrypt_pk's).
+    const uint32_t full = L >= 32 ? ~0u : (1u << L) - 1;
+    const NttJob* all = persist(set, enc_jobs(full));
+    auto plan = [&](uint32_t mask) {
+      if (mask != full && encrypt_limbs_supported((int)c->logn))
+        return std::make_pair(persist(set, enc_jobs(mask)), mask);
+      return std::make_pair(all, full);
+    };
+    std::tie(set->d_enc_r, set->enc_mask_r) = plan(((1u << nl_r) - 1) | (L >= 2 ? 1u << (L - 1) : 0u));
+    std::tie(set->d_enc_n, set->enc_mask_n) = plan((1u << nl_n) - 1);
+  }
   // rescaled products straight into segment sums (rescale_decrypt_kernel)
   // where the decryption reads limb 0 and its transform can sum the segments
   const bool fused_rd = L >= 2 && nl_r == 1 && segsum_in_transform(c, nb, cols);
@@ -2129,11 +2156,12 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
   {
     NttArgs ea{};
     ea.lc = ctx->d_lc;
-    ea.jobs = set->d_enc_ntt;
+    ea.jobs = do_rescale ? set->d_enc_r : set->d_enc_n;
     ea.load = NTT_LOAD_ENC;
     ea.bc = ctx->d_bc;
     bool combined = false;
-    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, pk_pairs(ctx, pk), set->cts, &combined, st));
+    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, do_rescale ? set->enc_mask_r : set->enc_mask_n,
+                          pk_pairs(ctx, pk), set->cts, &combined, st));
     if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
   }
   if (do_rescale && set->d_rd) {

@@ -116,14 +116,19 @@ hipError_t allow_full_lds() {
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
-// The forward transforms of ninputs encrypt_pk inputs: a is the NTT_LOAD_ENC job
-// list (3L jobs per input, M_0..M_{L-1}, E1_0.., U_0..). At split sizes the
-// row passes also combine them with the public key, given as prepared pairs
-// pkp of [b | a] (launch_prepare_pairs), into the ciphertexts at
-// cts + i 2 L N (*combined = true, k_encrypt_combine not needed); otherwise
-// the transforms are written to the jobs' dst and *combined = false.
-hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, const uint64_t* pkp,
-                          uint64_t* cts, bool* combined, hipStream_t s);
+// The forward transforms of ninputs encrypt_pk inputs on the limbs in
+// limb_mask (bit l: limb l; n of them): a is the NTT_LOAD_ENC job list (3n
+// jobs per input, M, E1 and U of each of those limbs in increasing order). At
+// split sizes the row passes also combine them with the public key, given as
+// prepared pairs pkp of [b | a] (launch_prepare_pairs), into those limbs of
+// the ciphertexts at cts + i 2 L N (*combined = true, k_encrypt_combine not
+// needed); otherwise (all L limbs only) the transforms are written to the
+// jobs' dst and *combined = false. Limb subsets take the split kernels,
+// which exist for the sizes encrypt_limbs_supported accepts.
+hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
+                          const uint64_t* pkp, uint64_t* cts, bool* combined, hipStream_t s);
+// Whether launch_encrypt takes limb subsets at transform size 2^logn.
+bool encrypt_limbs_supported(int logn);
 // The two transform launches of an evaluation-domain rescale: ninv inverse
 // transforms (inv, store NONE) of the products' last limbs, then nfwd forward
 // transforms (fwd, load REDUCE) of each last limb reduced modulo the lower

@@ -273,6 +273,56 @@ def test_lora_set_crt_branch_after_rescale():
     _check(got, got_sums, exp, exp_sums)
 
 
+@pytest.mark.parametrize("n, moduli, d", [
+    (16384, [1125899904679937, 1099507695617, 1152921504598720513], 1536),
+    (16384, [1099507695617, 1099506515969, 1152921504598720513], 1536),
+    (4096, [1152921504606584833, 1099507695617, 1152921504598720513], 512),
+])
+def test_lora_set_rescale_decrypt_chains(n, moduli, d):
+    """Rescaled sets whose decryption reads limb 0 rescale and decrypt each batch in one kernel
+    after the last limb's inverse transforms: INTT(D pt - NTT(r1) s) - r0, times q_last^-1.
+    Chains: a 50-bit limb 0 below a 60-bit last prime (the last limb's values are reduced by
+    Barrett, not passed through), a 40-bit limb 0 (FP64 transforms), and N=4096. The segment
+    sums equal th_lora_a_pass's (the full rescale, then the decryption) bit for bit, and the
+    deltas match the oracle's."""
+    eng, ref = tensafe_he.CkksContext(n, moduli=moduli), orc.Context(n, moduli=moduli)
+    sk, rsk = eng.keygen(seed=5), ref.keygen(5)
+    pk, rpk = eng.keygen_public(sk, seed=6), ref.keygen_public(rsk, 6)
+    rng = np.random.default_rng(n + moduli[0] % 1000)
+    H = rng.normal(size=(2, d)) * 0.1
+    proj = _projections(rng, 2, d, ranks=[16, 7], d_outs=[24, 9])
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    seeds = [31, 32]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=True, with_intermediates=True)
+    packs = [(i, zero_moai.pack_rows(A, n // 2)) for i, A, _ in proj]
+    pts = [eng.encode_to_ntt(p) for _, ps in packs for p in ps]
+    pin = [i for i, ps in packs for _ in ps]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=True), got_sums)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, True)
+    _check(got, got_sums, exp, exp_sums)
+
+
+def test_lora_set_many_batches_rescale(env):
+    """260 batches, more than one round of whole-polynomial workgroups: the rescale of the limbs
+    the decryption reads runs on the split kernels and a separate decryption follows. The
+    segment sums equal th_lora_a_pass's bit for bit; the first two projections match the
+    oracle."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(17)
+    H = rng.normal(size=(2, 1536)) * 0.1
+    proj = _projections(rng, 2, 1536, ranks=[20] * 65, d_outs=[4] * 65)
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    assert ls.n_batches == 260
+    seeds = [51, 52]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=True, with_intermediates=True)
+    packs = [(i, zero_moai.pack_rows(A, 8192)) for i, A, _ in proj]
+    pts = [eng.encode_to_ntt(p) for _, ps in packs for p in ps]
+    pin = [i for i, ps in packs for _ in ps]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=True), got_sums)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj[:2], True)
+    _check(got[:2], got_sums[:8], exp, exp_sums)
+
+
 def test_lora_set_serial_sampler_path(env):
     """Forcing every input through the serial replay (the path a rejected range_u32 word
     takes) gives the same deltas, and the per-input reject flags are cleared afterwards."""
