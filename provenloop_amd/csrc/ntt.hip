@@ -50,7 +50,7 @@ hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t n
 hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf,
                                 hipStream_t s);
 hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
-                                const uint64_t* pkp, uint64_t* cts, hipStream_t s);
+                                const EncDot& dot, const uint64_t* pkp, uint64_t* cts, hipStream_t s);
 
 template <int LOGN>
 struct Shape {
@@ -470,18 +470,18 @@ hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const Ntt
 bool encrypt_limbs_supported(int logn) { return logn >= NTT_SPLIT_MIN_LOGN && logn <= NTT_MAX_LOGN; }
 
 hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
-                          const uint64_t* pkp, uint64_t* cts, bool* combined, hipStream_t s) {
+                          const EncDot& dot, const uint64_t* pkp, uint64_t* cts, bool* combined, hipStream_t s) {
   *combined = false;
   if (ninputs == 0) return hipSuccess;
   const uint32_t nl = (uint32_t)__builtin_popcount(limb_mask);
-  if (nl == 0 || limb_mask >> L) return hipErrorInvalidValue;
-  // the split kernels also serve limb subsets (k_encrypt_combine forms every limb)
-  const bool split = use_split(logn, ninputs * 3 * nl) || (nl != L && encrypt_limbs_supported(logn));
+  if (nl == 0 || limb_mask >> L || (dot.mask & ~limb_mask)) return hipErrorInvalidValue;
+  // the split kernels also serve limb subsets and D (k_encrypt_combine forms every limb of c0 and c1)
+  const bool split = use_split(logn, ninputs * 3 * nl) || ((nl != L || dot.mask) && encrypt_limbs_supported(logn));
   if (split && a.jobs && a.load == NTT_LOAD_ENC && a.store == NTT_STORE_NONE) {
     *combined = true;
-    return launch_encrypt_split(logn, a, ninputs, L, limb_mask, pkp, cts, s);
+    return launch_encrypt_split(logn, a, ninputs, L, limb_mask, dot, pkp, cts, s);
   }
-  if (nl != L) return hipErrorInvalidValue;  // k_encrypt_combine forms every limb
+  if (nl != L || dot.mask) return hipErrorInvalidValue;  // k_encrypt_combine forms every limb, no D
   return launch_ntt(logn, false, a, ninputs * 3 * L, s);
 }
 

@@ -477,10 +477,13 @@ hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, con
 // store c0 and c1. The limbs are those in mask (n of them); jobs: 3n per
 // input (M, E1 and U of each of those limbs in increasing order);
 // pkp = [b (L) | a (L)] as prepared pairs (w, companion), so each product is
-// one Shoup or FP64 step; input i's ciphertext at cts + i 2 L N.
+// one Shoup or FP64 step; input i's ciphertext at cts + i 2 L N. On the limbs
+// in dot.mask the kernel stores D = c0 + c1 s instead (EncDot): M's and E1's
+// wavefronts each hand the other half of their outputs over through LDS and
+// form D on their own half.
 template <int LOGN>
 __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint64_t* pkp, uint64_t* cts, uint32_t L,
-                                                          uint32_t mask) {
+                                                          uint32_t mask, EncDot dot) {
   using S = Split<LOGN>;
   __shared__ uint64_t lds[3][S::LDS];
   const uint32_t nl = (uint32_t)__builtin_popcount(mask);
@@ -496,6 +499,7 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
   const BarrettConst bc = a.bc[l];
   const size_t off = (size_t)l * S::N + ((size_t)part << 10) + lane;
   uint64_t* shared_u = lds[1];
+  const bool form_d = (dot.mask >> l) & 1;  // uniform over the workgroup
   auto run = [&]<class A>() {
     const A ar(lc);
     typename A::V x[16];
@@ -513,6 +517,7 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
       for (int k = 0; k < 16; ++k) shared_u[lane + 64 * k] = ar.fwd_store(x[k]);
     }
     __syncthreads();
+    uint64_t c[16];  // M's and E1's wavefronts keep c0, c1 where D is formed
     if (wv != 1) {
       const GMut<uint64_t> out = gst(cts + (size_t)i * 2 * L * S::N + (wv == 0 ? 0 : (size_t)L * S::N)) + off;
 #pragma unroll
@@ -530,7 +535,37 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
           r = shoup_approx(u, p.w, p.ws, bc.q) + m;  // [0, 5q)
           r = csub(csub(csub(r, 4 * bc.q), 2 * bc.q), bc.q);
         }
-        out[64 * k] = r;
+        if (!form_d) {
+          out[64 * k] = r;
+        } else {
+          // M's wavefront forms D on elements 0..7 and hands c0 of 8..15 to
+          // E1's, which forms D on 8..15 (its own slice, free once its passes
+          // are done, holds the exchange)
+          c[k] = r;
+          if ((wv == 0) == (k >= 8)) lds[2][lane + 64 * k] = r;
+        }
+      }
+    }
+    if (form_d) {
+      // D = c0 + c1 s in [0, 3q) (the key in Montgomery form), at input i's
+      // slot for this limb: the position of l among dot.mask's limbs
+      const uint32_t kd = (uint32_t)__builtin_popcount(dot.mask & ((1u << l) - 1));
+      const uint32_t nd = (uint32_t)__builtin_popcount(dot.mask);
+      const GPtr<uint64_t> key = gld(dot.skm) + off;
+      const GMut<uint64_t> dst = gst(dot.out) + ((size_t)i * nd + kd) * S::N + ((size_t)part << 10) + lane;
+      uint64_t sv[8];
+      const int k0 = wv == 0 ? 0 : 8;
+      if (wv != 1) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sv[k] = key[64 * (k0 + k)];
+      }
+      __syncthreads();
+      if (wv == 0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dst[64 * k] = c[k] + mont_mul(lds[2][lane + 64 * k], sv[k], bc);
+      } else if (wv == 2) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dst[64 * (8 + k)] = lds[2][lane + 64 * (8 + k)] + mont_mul(c[8 + k], sv[k], bc);
       }
     }
   };
@@ -541,23 +576,23 @@ __global__ __launch_bounds__(192) void encrypt_row_kernel(NttArgs a, const uint6
 }
 
 template <int LOGN>
-static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t mask, const uint64_t* pkp,
-                                   uint64_t* cts, hipStream_t s) {
+static hipError_t launch_encrypt_t(const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t mask, const EncDot& dot,
+                                   const uint64_t* pkp, uint64_t* cts, hipStream_t s) {
   using S = Split<LOGN>;
   const uint32_t nl = (uint32_t)__builtin_popcount(mask);
   hipLaunchKernelGGL((ntt_split_kernel<LOGN, false, true, NTT_LOAD_ENC, NTT_STORE_NONE>),
                      dim3(ninputs * 3 * nl * S::PARTS), dim3(64), 0, s, a);
   hipLaunchKernelGGL((encrypt_row_kernel<LOGN>), dim3(ninputs * nl * S::PARTS), dim3(192), 0, s, a, pkp, cts, L,
-                     mask);
+                     mask, dot);
   return hipGetLastError();
 }
 
 hipError_t launch_encrypt_split(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
-                                const uint64_t* pkp, uint64_t* cts, hipStream_t s) {
+                                const EncDot& dot, const uint64_t* pkp, uint64_t* cts, hipStream_t s) {
   switch (logn) {
-    case 13: return launch_encrypt_t<13>(a, ninputs, L, limb_mask, pkp, cts, s);
-    case 14: return launch_encrypt_t<14>(a, ninputs, L, limb_mask, pkp, cts, s);
-    case 15: return launch_encrypt_t<15>(a, ninputs, L, limb_mask, pkp, cts, s);
+    case 13: return launch_encrypt_t<13>(a, ninputs, L, limb_mask, dot, pkp, cts, s);
+    case 14: return launch_encrypt_t<14>(a, ninputs, L, limb_mask, dot, pkp, cts, s);
+    case 15: return launch_encrypt_t<15>(a, ninputs, L, limb_mask, dot, pkp, cts, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -2153,24 +2153,35 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
   HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
                        ctx->d_stage_im, ctx->logn, L, st, z, fix_in_encode ? set->d_sample : nullptr, seeds,
                        ctx->force_serial, band));
+  // D = c0 + c1 s, all the decryption reads of an input's limbs 0..nl-1
+  // (k_key_dot, or formed by the encrypt row passes in place of those limbs
+  // where they run): limb 0 before the fused rescale-decrypt, limbs
+  // 0..nl_n-1 without a rescale
+  const bool fused_rd = do_rescale && set->d_rd;
+  const uint32_t nl_d = fused_rd ? 1 : (do_rescale ? 0 : set->nl_n);
+  const uint64_t* skm = nl_d ? sk_montgomery(ctx, sk) : nullptr;
+  bool d_formed = false;
   {
     NttArgs ea{};
     ea.lc = ctx->d_lc;
     ea.jobs = do_rescale ? set->d_enc_r : set->d_enc_n;
     ea.load = NTT_LOAD_ENC;
     ea.bc = ctx->d_bc;
+    EncDot dot{};
+    if (nl_d && encrypt_limbs_supported((int)ctx->logn)) dot = EncDot{(1u << nl_d) - 1, skm, set->dkey};
     bool combined = false;
-    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, do_rescale ? set->enc_mask_r : set->enc_mask_n,
+    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, do_rescale ? set->enc_mask_r : set->enc_mask_n, dot,
                           pk_pairs(ctx, pk), set->cts, &combined, st));
     if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
+    d_formed = combined && dot.mask;
   }
+  if (nl_d && !d_formed)
+    HIPCHK(launch_key_dot(set->cts, (uint64_t)2 * L * N, skm, set->dkey, ctx->d_bc, N, L, nl_d, ni, st));
   if (do_rescale && set->d_rd) {
     // the last limb of (c0 pt, c1 pt) as coefficients (ct x pt in the inverse
     // transforms' loads), D = c0 + c1 s on limb 0 per input, then each batch's
     // rescale and decryption on limb 0 in one kernel, which writes the sums
     launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MULM);
-    const uint64_t* skm = sk_montgomery(ctx, sk);
-    HIPCHK(launch_key_dot(set->cts, (uint64_t)2 * L * N, skm, set->dkey, ctx->d_bc, N, L, 1, ni, st));
     RescaleDecryptArgs ra{};
     ra.lc = ctx->d_lc;
     ra.bc = ctx->d_bc;
@@ -2194,10 +2205,8 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * set->nl_r, st));
     if (!set->d_dot_seg) launch_jobs_ntt(ctx, true, set->d_dot_r, set->dot_r_jobs, NTT_LOAD_DOT, nullptr, sk->d);
   } else {
-    // the product ciphertexts (c0 pt, c1 pt) decrypt to pt (c0 + c1 s): D once
-    // per input, then each batch's inverse transforms with pt * D in their loads
-    HIPCHK(launch_key_dot(set->cts, (uint64_t)2 * L * N, sk_montgomery(ctx, sk), set->dkey, ctx->d_bc, N, L,
-                          set->nl_n, ni, st));
+    // the product ciphertexts (c0 pt, c1 pt) decrypt to pt (c0 + c1 s): with
+    // D (above), each batch's inverse transforms with pt * D in their loads
     launch_jobs_ntt(ctx, true, set->d_inv_nr, set->inv_nr_jobs, NTT_LOAD_MULM);
   }
   const DecodeJob* dec = do_rescale ? set->d_dec_r : set->d_dec_n;

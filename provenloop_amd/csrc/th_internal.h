@@ -116,6 +116,16 @@ hipError_t allow_full_lds() {
 
 // Launch njobs forward (inverse=false) or inverse negacyclic NTTs of size 2^logn.
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
+// The decryption's D = c0 + c1 s (in [0, 3q)), formed by the encrypt row
+// passes on the limbs in mask instead of storing c0 and c1 there: input i's D
+// on the k-th limb of mask at out + (i n + k) N for n limbs in mask; skm =
+// the secret key (L x N) in Montgomery form.
+struct EncDot {
+  uint32_t mask;
+  const uint64_t* skm;
+  uint64_t* out;
+};
+
 // The forward transforms of ninputs encrypt_pk inputs on the limbs in
 // limb_mask (bit l: limb l; n of them): a is the NTT_LOAD_ENC job list (3n
 // jobs per input, M, E1 and U of each of those limbs in increasing order). At
@@ -123,10 +133,12 @@ hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, 
 // prepared pairs pkp of [b | a] (launch_prepare_pairs), into those limbs of
 // the ciphertexts at cts + i 2 L N (*combined = true, k_encrypt_combine not
 // needed); otherwise (all L limbs only) the transforms are written to the
-// jobs' dst and *combined = false. Limb subsets take the split kernels,
-// which exist for the sizes encrypt_limbs_supported accepts.
+// jobs' dst and *combined = false. Limb subsets and dot (limbs of limb_mask
+// whose D is formed in place of the ciphertext) take the split kernels, which
+// exist for the sizes encrypt_limbs_supported accepts (other sizes: all
+// limbs and no D only).
 hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t L, uint32_t limb_mask,
-                          const uint64_t* pkp, uint64_t* cts, bool* combined, hipStream_t s);
+                          const EncDot& dot, const uint64_t* pkp, uint64_t* cts, bool* combined, hipStream_t s);
 // Whether launch_encrypt takes limb subsets at transform size 2^logn.
 bool encrypt_limbs_supported(int logn);
 // The two transform launches of an evaluation-domain rescale: ninv inverse
