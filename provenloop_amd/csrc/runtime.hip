@@ -118,6 +118,7 @@ class StagingRing {
   void init(size_t bytes) {
     cap_ = bytes;
     HIPCHK(hipHostMalloc(&host_, cap_, hipHostMallocDefault));
+    memset(host_, 0, cap_);  // touched once here rather than by the first copies through each page
     off_ = 0;
   }
   void destroy() {
@@ -302,6 +303,10 @@ struct th_lora {
   const MoeBatch* d_moe_b = nullptr;
   const MoeProj* d_moe_p = nullptr;
   uint32_t max_b_count = 0;
+  // pinned host staging of host-I/O tokens (hidden states in, deltas and
+  // segment sums out), the same pages every token
+  void* io_host = nullptr;
+  size_t io_bytes = 0;
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
     owned.push_back(p);
@@ -2121,11 +2126,19 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->d_bjobs = persist(set, bj);
   if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
   if (set->d_dot_seg || set->d_rd) set->seg_p = seg_pairs(c, d);
+  // Host-I/O tokens stage through one pinned buffer of the set, written once
+  // here: a token staged through fresh pinned pages (the context's ring on
+  // its first pass) measured about twice the time of one staged through
+  // pages used before.
+  set->io_bytes = std::max((size_t)ni * d * 8, (size_t)(set->n_deltas + (uint64_t)nb * cols) * 8);
+  HIPCHK(hipHostMalloc(&set->io_host, set->io_bytes, hipHostMallocDefault));
+  memset(set->io_host, 0, set->io_bytes);
   HIPCHK(hipStreamSynchronize(c->stream));
 }
 
 void free_lora(th_lora* set) {
   th_ctx* c = set->ctx;
+  if (set->io_host) (void)hipHostFree(set->io_host);
   for (void* p : set->owned) c->pool.put(p);
   delete set;
   ctx_release(c);
@@ -2348,9 +2361,9 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     // device-resident inputs are read where they are; host inputs go through one copy
     const double* z = hidden;
     if (!hidden_on_device) {
-      void* h = ctx->ring.reserve(hbytes, st);
-      memcpy(h, hidden, hbytes);
-      HIPCHK(hipMemcpyAsync(set->hidden, h, hbytes, hipMemcpyHostToDevice, st));
+      // the set's staging buffer is free: every host-I/O call waits for its copies
+      memcpy(set->io_host, hidden, hbytes);
+      HIPCHK(hipMemcpyAsync(set->hidden, set->io_host, hbytes, hipMemcpyHostToDevice, st));
       z = set->hidden;
     }
     double* dout = deltas_on_device ? deltas : set->deltas;
@@ -2373,7 +2386,7 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     }
     const size_t db = set->n_deltas * 8, ib = (size_t)nb * set->cols * 8;
     if (!deltas_on_device || inter) {
-      char* hh = (char*)ctx->ring.reserve(db + ib, st);
+      char* hh = (char*)set->io_host;  // stream order: after the hidden states' copy
       if (!deltas_on_device) HIPCHK(hipMemcpyAsync(hh, set->deltas, db, hipMemcpyDeviceToHost, st));
       if (inter) HIPCHK(hipMemcpyAsync(hh + db, set->sums, ib, hipMemcpyDeviceToHost, st));
       wait_stream(ctx);
