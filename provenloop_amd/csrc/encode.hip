@@ -71,6 +71,7 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
   }
   // input gather, 8 values per thread per round: all loads issued before the
   // first LDS store
+  const double g = jb.gate ? *gld(jb.gate) : 1.0;
   for (uint32_t j0 = threadIdx.x; j0 < M; j0 += FV * blockDim.x) {
     double v[FV];
 #pragma unroll
@@ -85,7 +86,8 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
         keep = keep && slot < jb.rep_cols * jb.rep_d;
         idx = keep ? slot % jb.rep_d : 0;
       }
-      const double t = z[idx];  // unconditional (index 0 when unused), so the loads issue together
+      double t = z[idx];  // unconditional (index 0 when unused), so the loads issue together
+      if (jb.gate) t = slot < jb.n_valid ? g * t : 0.0;  // the same f64 products as gating on the host
       v[e] = keep ? t : 0.0;
     }
 #pragma unroll

@@ -13,8 +13,11 @@ struct EncodeJob {
   const int64_t* e1;   // rounded Gaussian e1, or null
   uint64_t* dst;       // [M (L) | E1 (L) | U (L)] limb-polys; only M when e1/u are null
   int64_t* mvals;      // non-null: write m itself (N i64) instead of dst (the residues are then
-                       // formed by the encrypt transforms' loads, NTT_LOAD_ENC)
+                       // formed by the transforms' loads, NTT_LOAD_ENC or NTT_LOAD_MSUM)
   double* parts;       // scratch, encode_parts_doubles(logn) doubles
+  const double* gate;  // non-null (no replication): slots are gate[0] * z[slot] for slot < n_valid,
+                       // 0 beyond (a gated expert's packed rows, inference_engine.py:1300-1308)
+  uint32_t n_valid;
 };
 
 struct SampleJob;

@@ -29,23 +29,6 @@ hipError_t launch_lora_b(const LoraBJob* jobs, uint32_t njobs, uint32_t max_d_ou
   return hipGetLastError();
 }
 
-// Gated expert rows of a mixture set: slot vector (b, x) of the output is
-// g[proj(b) * k + x] times the packed A rows of expert x in batch b, in its
-// first n_valid slots (the rows the batch holds), and 0 beyond: the same f64
-// products as packing g * A rows on the host (inference_engine.py:1300-1308).
-__global__ __launch_bounds__(256) void k_moe_gate_pack(const double* __restrict__ apack,
-                                                       const MoeBatch* __restrict__ batches,
-                                                       const double* __restrict__ gates, uint32_t k, uint32_t slots,
-                                                       double* __restrict__ out) {
-  const uint32_t v = blockIdx.y;  // batch v / k, expert v % k
-  const MoeBatch mb = batches[v / k];
-  const double g = gates[(size_t)mb.proj * k + v % k];
-  const double* a = apack + (size_t)v * slots;
-  double* o = out + (size_t)v * slots;
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < slots; i += gridDim.x * blockDim.x)
-    o[i] = i < mb.n_valid ? g * a[i] : 0.0;
-}
-
 // B of each projection mixed over its experts, sum_x g_x B_x, accumulated
 // from 0.0 in expert order as separate multiplies and adds (rank-major, as the
 // experts' B are stored).
@@ -62,15 +45,6 @@ __global__ __launch_bounds__(256) void k_moe_mix_b(const double* __restrict__ be
     }
     bmix[mp.off + t] = acc;
   }
-}
-
-hipError_t launch_moe_gate_pack(const double* apack, const MoeBatch* batches, const double* gates, uint32_t nb,
-                                uint32_t k, uint32_t slots, double* out, hipStream_t s) {
-  if (!nb) return hipSuccess;
-  uint32_t bx = (slots + 255) / 256;
-  if (bx > 32) bx = 32;
-  hipLaunchKernelGGL(k_moe_gate_pack, dim3(bx, nb * k), dim3(256), 0, s, apack, batches, gates, k, slots, out);
-  return hipGetLastError();
 }
 
 hipError_t launch_moe_mix_b(const double* bexp, const MoeProj* projs, const double* gates, uint32_t n_proj, uint32_t k,

@@ -307,7 +307,7 @@ __device__ __forceinline__ void run_ntt(const uint64_t* __restrict__ src, uint64
 #pragma unroll
     for (int k = 0; k < S::E; ++k) {
       const uint32_t i = elem<S::LE, S::WAVE_LO>(tid, k);
-      gdst[i] = so.apply(ar, x[k], i);
+      so.store(ar, x[k], gdst, i, so.prep(ar, so.load_aux(i)));
     }
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));

@@ -96,8 +96,9 @@ struct LoadOp {
   const uint64_t* key;  // secret-key limb-poly (DOT)
   BarrettConst bc;
   RescaleConst rc;
-  uint32_t sub;         // ENC variant (uniform over the job)
-  double qd, qinv;      // q and 1/q as doubles (ENC)
+  uint32_t sub;         // ENC variant, MSUM vector count (uniform over the job)
+  uint32_t n;           // transform size (MSUM: stride of the vectors)
+  double qd, qinv;      // q and 1/q as doubles (ENC, MSUM)
   // signed_residue_dev with |e| in [q, 2^53) reduced by one exact FP64 step:
   // quot = rint(|e| / q) is within one of the true quotient, and the remainder
   // fma(-quot, q, |e|) is an exact integer in (-q, q)
@@ -170,6 +171,12 @@ struct LoadOp {
   }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
     if constexpr (LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM) return finish(fetch(src, i));
+    if constexpr (LD == NTT_LOAD_MSUM) {
+      const GPtr<int64_t> m = gld(reinterpret_cast<const int64_t*>(src));
+      uint64_t acc = 0;
+      for (uint32_t e = 0; e < sub; ++e) acc = addmod(acc, enc_residue(m[(size_t)e * n + i]), bc.q);
+      return acc;
+    }
     const uint64_t x = gld(src)[i];
     if constexpr (LD == NTT_LOAD_DOTM) return x + mont_mul(gld(aux)[i], gld(key)[i], bc);
     if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
@@ -196,6 +203,19 @@ struct StoreOp {
   // rescale subtracts from); loaded apart from the arithmetic so that a pass
   // can issue these loads early and hide their latency behind its butterflies.
   static constexpr int NAUX = ST == NTT_STORE_MUL_RESCALE ? 2 : ST == NTT_STORE_RESCALE ? 1 : 0;
+  // Store of transform output x at position i of dst (MONT: its Montgomery
+  // form, and the plain residue to aux when aux is set).
+  template <class A>
+  __device__ __forceinline__ void store(const A& ar, typename A::V x, GMut<uint64_t> dst, uint32_t i,
+                                        uint64_t cp) const {
+    if constexpr (ST == NTT_STORE_MONT) {
+      const uint64_t y = ar.fwd_store(x);
+      dst[i] = mulmod_barrett(y, bc.r64, bc);
+      if (aux) gst(const_cast<uint64_t*>(aux))[i] = y;
+    } else {
+      dst[i] = apply_prep(ar, x, cp);
+    }
+  }
   struct Aux {
     uint64_t a, b;
   };
@@ -245,10 +265,6 @@ struct StoreOp {
         return csub(shoup_lazy(submod(cp, y, rc.q), rc.inv, rc.inv_s, rc.q), rc.q);
     }
   }
-  template <class A>
-  __device__ __forceinline__ uint64_t apply(const A& ar, typename A::V x, uint32_t i) const {
-    return apply_prep(ar, x, prep(ar, load_aux(i)));
-  }
 };
 
 // Load and store operations of job `jb` in launch `a` for limb `limb`.
@@ -257,10 +273,11 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
                                         LoadOp<LD>& op, StoreOp<ST>& so) {
   op.aux = jb.aux;
   if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT || LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM ||
-                LD == NTT_LOAD_DOTM)
+                LD == NTT_LOAD_DOTM || LD == NTT_LOAD_MSUM)
     op.bc = a.bc[limb];
-  if constexpr (LD == NTT_LOAD_ENC) {
+  if constexpr (LD == NTT_LOAD_ENC || LD == NTT_LOAD_MSUM) {
     op.sub = jb.sub;
+    op.n = n;
     op.qd = a.lc[limb].qd;
     op.qinv = a.lc[limb].qinv;
   }
@@ -269,7 +286,7 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
   so.aux = jb.aux;
   so.aux2 = jb.aux2;
   if constexpr (ST == NTT_STORE_RESCALE || ST == NTT_STORE_MUL_RESCALE) so.rc = a.rc[limb];
-  if constexpr (ST == NTT_STORE_MUL_RESCALE) so.bc = a.bc[limb];
+  if constexpr (ST == NTT_STORE_MUL_RESCALE || ST == NTT_STORE_MONT) so.bc = a.bc[limb];
   if constexpr (ST == NTT_STORE_SEGSUM) {
     so.segw = a.segw;
     so.seg = reinterpret_cast<double*>(jb.dst);
@@ -280,8 +297,8 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE | ENC,
-// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE); inverse (NONE | MUL |
-// MULM | DOT, NONE), (DOT | DOTM, SEGSUM).
+// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE), (MSUM, MONT); inverse
+// (NONE | MUL | MULM | DOT, NONE), (DOT | DOTM, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   if constexpr (!INV) {
@@ -291,6 +308,7 @@ __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_RESCALE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_MUL_RESCALE)
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_MUL_RESCALE>();
+    if (load == NTT_LOAD_MSUM && store == NTT_STORE_MONT) return f.template operator()<NTT_LOAD_MSUM, NTT_STORE_MONT>();
     return hipErrorInvalidValue;
   } else {
     if (load == NTT_LOAD_DOT && store == NTT_STORE_SEGSUM)

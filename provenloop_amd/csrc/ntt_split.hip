@@ -301,7 +301,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     fwd_stages<LOGN, 0, CB - 5, 0, A, (SOp::NAUX > 0)>(x, jbase + p2(0), tw, ar);
     wave_exchange(x, lds, p2, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) gdst[jbase + g(k)] = so.apply_prep(ar, x[k], c[NP > 1 ? k : 0]);
+    for (int k = 0; k < 16; ++k) so.store(ar, x[k], gdst, jbase + g(k), c[NP > 1 ? k : 0]);
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
     if constexpr (LOp::kind == NTT_LOAD_MULM) {

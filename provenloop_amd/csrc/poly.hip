@@ -43,24 +43,6 @@ __global__ void k_ct_addsub(const AddJob* __restrict__ jobs, const uint64_t* __r
   }
 }
 
-// dst[b][l][i] = sum over x < k of src[b * k + x][l][i] mod q_l: k plaintexts
-// (NTT domain, L limbs each) folded into one. ct * p_0 + ... + ct * p_{k-1}
-// (ct_pt_mul_ntt then ct_add, ciphertext.rs:422-429, :435-450) equals
-// ct * (p_0 + ... + p_{k-1}) mod q_l residue by residue, so a product with the
-// folded plaintext is bit-identical to the sum of the k products.
-__global__ void k_pt_sum(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
-                         const uint64_t* __restrict__ q, uint32_t k, uint32_t nb, uint32_t L, uint32_t n) {
-  const uint64_t per = (uint64_t)L * n;
-  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nb * per; e += (uint64_t)gridDim.x * blockDim.x) {
-    const uint64_t b = e / per, r = e - b * per;
-    const uint64_t m = q[r / n];
-    const uint64_t* x = src + b * k * per + r;
-    uint64_t acc = x[0];
-    for (uint32_t j = 1; j < k; ++j) acc = addmod(acc, x[(uint64_t)j * per], m);
-    dst[e] = acc;
-  }
-}
-
 // Operands fixed for many products (keys) prepared as pairs in the twiddle
 // tables' formats: (w, floor(w 2^64 / q)) on the integer limbs, (w, w / q as
 // a double) on limbs below 2^41, so a product by w is one Shoup or one FP64
@@ -179,15 +161,6 @@ hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_lim
                             uint32_t n, hipStream_t s) {
   if (!njobs) return hipSuccess;
   hipLaunchKernelGGL(k_ct_addsub, grid_for(2 * max_limbs * n, njobs), dim3(256), 0, s, jobs, q, n);
-  return hipGetLastError();
-}
-
-hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, uint32_t k, uint32_t nb, uint32_t L,
-                         uint32_t n, hipStream_t s) {
-  if (!nb) return hipSuccess;
-  const uint64_t total = (uint64_t)nb * L * n;
-  const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255) / 256, 4096);
-  hipLaunchKernelGGL(k_pt_sum, dim3(blocks), dim3(256), 0, s, src, dst, q, k, nb, L, n);
   return hipGetLastError();
 }
 

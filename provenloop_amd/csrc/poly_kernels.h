@@ -78,9 +78,6 @@ struct MoeProj {
   uint32_t count;
   uint32_t pad_;
 };
-// out (nb*k x slots) = gate-scaled packed A rows of every batch and expert (k_moe_gate_pack).
-hipError_t launch_moe_gate_pack(const double* apack, const MoeBatch* batches, const double* gates, uint32_t nb,
-                                uint32_t k, uint32_t slots, double* out, hipStream_t s);
 // bmix = sum_x g_x B_x per projection (k_moe_mix_b).
 hipError_t launch_moe_mix_b(const double* bexp, const MoeProj* projs, const double* gates, uint32_t n_proj, uint32_t k,
                             uint32_t max_count, double* bmix, hipStream_t s);
@@ -89,9 +86,6 @@ hipError_t launch_ct_pt_mul(const CtPtJob* jobs, uint32_t njobs, uint32_t max_li
                             uint32_t n, hipStream_t s);
 hipError_t launch_ct_addsub(const AddJob* jobs, uint32_t njobs, uint32_t max_limbs, const uint64_t* q,
                             uint32_t n, hipStream_t s);
-// dst (nb x L x N) = per-batch sums mod q of k consecutive plaintexts in src (nb*k x L x N).
-hipError_t launch_pt_sum(const uint64_t* src, uint64_t* dst, const uint64_t* q, uint32_t k, uint32_t nb, uint32_t L,
-                         uint32_t n, hipStream_t s);
 // pk (optional): the public key [b | a] for every job instead of the jobs' fields.
 // D = c0 + c1 s (lazy, [0, 3q)) on limbs 0..nl-1 of count ciphertexts, key in Montgomery form (k_key_dot).
 hipError_t launch_key_dot(const uint64_t* cts, uint64_t ct_stride, const uint64_t* skm, uint64_t* out,

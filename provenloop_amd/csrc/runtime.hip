@@ -300,9 +300,13 @@ struct th_lora {
   const double* apack = nullptr;  // n_batches x k x N/2: the experts' packed A rows, ungated
   const double* bexp = nullptr;   // the experts' B, rank-major (MoeProj)
   double* bmix = nullptr;         // sum_x g_x B_x: what the B jobs read
-  const MoeBatch* d_moe_b = nullptr;
   const MoeProj* d_moe_p = nullptr;
   uint32_t max_b_count = 0;
+  std::vector<MoeBatch> moe_b;     // per batch: projection and rows (host copy)
+  double* d_gates = nullptr;       // n_proj x k, the current gates
+  int64_t* moe_m = nullptr;        // n_batches x k x N: the experts' encoded vectors m
+  const NttJob* d_moe_ntt = nullptr;  // per batch and plaintext limb: sum of the k m, transform, Montgomery copy
+  uint32_t moe_ntt_jobs = 0;
   // pinned host staging of host-I/O tokens (hidden states in, deltas and
   // segment sums out), the same pages every token
   void* io_host = nullptr;
@@ -1867,30 +1871,51 @@ void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, Nt
   HIPCHK(launch_ntt((int)c->logn, inverse, a, n, c->stream));
 }
 
-// Queue the plaintexts and mixed B of a mixture set for the gates g (device,
+// Queue the plaintexts and mixed B of a mixture set for its gates (set->d_gates,
 // n_proj x k): every batch's plaintext is sum_x encode_to_ntt(g_x * A_x rows)
-// (the encoder and transforms of th_encode_to_ntt), then its Montgomery form,
-// and B = sum_x g_x B_x. The transform is linear mod q, so the k encoded
-// residue polynomials are summed first (launch_pt_sum) and transformed once
-// per batch and limb: the same residues as summing the k transforms.
-void queue_regate(OpScope& sc, th_lora* set, const double* g) {
+// (the encoder and transforms of th_encode_to_ntt), in Montgomery form (and
+// plain where a token reads it), and B = sum_x g_x B_x. The encoder gates the
+// experts' packed rows as it reads them and writes each vector's m (i64); the
+// forward transform of each batch and plaintext limb sums the k residues
+// m_x mod q_l in its loads (NTT_LOAD_MSUM) and writes the Montgomery form in
+// its store (NTT_STORE_MONT). The transform is linear mod q_l, so this is the
+// sum of the k transforms, residue by residue. Only the limbs a token reads
+// are formed (set->d_moe_ntt).
+void queue_regate(OpScope& sc, th_lora* set) {
   th_ctx* c = sc.c;
-  const uint32_t N = c->N, S = N / 2, L = c->L, nb = set->n_batches, k = set->k;
-  double* z = (double*)sc.dev((size_t)nb * k * S * 8);
-  HIPCHK(launch_moe_gate_pack(set->apack, set->d_moe_b, g, nb, k, S, z, c->stream));
-  uint64_t* dst = (uint64_t*)sc.dev((size_t)nb * k * L * poly_bytes(c));
-  queue_encode(sc, z, (size_t)nb * k, nullptr, nullptr, nullptr, dst, (size_t)L * N);
-  HIPCHK(launch_pt_sum(dst, set->pts, c->d_q, k, nb, L, N, c->stream));
-  ntt_strided(c, false, set->pts, set->pts, nb * L, L);
-  HIPCHK(launch_to_montgomery(set->pts, set->ptm, c->d_bc, N, L, nb, c->stream));
-  HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, g, set->n_proj, k, set->max_b_count, set->bmix, c->stream));
+  const uint32_t N = c->N, S = N / 2, nb = set->n_batches, k = set->k;
+  const size_t nv = (size_t)nb * k, pd = encode_parts_doubles(c->logn);
+  double* parts = (double*)sc.dev(nv * pd * 8);
+  std::vector<EncodeJob> ej(nv);
+  for (size_t v = 0; v < nv; ++v) {
+    const MoeBatch& mb = set->moe_b[v / k];
+    ej[v].z = set->apack + v * S;
+    ej[v].gate = set->d_gates + (size_t)mb.proj * k + v % k;
+    ej[v].n_valid = mb.n_valid;
+    ej[v].mvals = set->moe_m + v * N;
+    ej[v].parts = parts + v * pd;
+  }
+  HIPCHK(launch_encode(sc.up(ej), (uint32_t)nv, c->d_bc, c->d_twist_re, c->d_twist_im, c->d_stage_re, c->d_stage_im,
+                       c->logn, c->L, c->stream));
+  launch_jobs_ntt(c, false, set->d_moe_ntt, set->moe_ntt_jobs, NTT_LOAD_MSUM, nullptr, nullptr, NTT_STORE_MONT);
+  HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, set->d_gates, set->n_proj, k, set->max_b_count, set->bmix,
+                          c->stream));
+}
+
+// New gates (host, n_proj x k) into the set's device copy, on the stream.
+void upload_gates(th_lora* set, const double* gates) {
+  th_ctx* c = set->ctx;
+  const size_t bytes = (size_t)set->n_proj * set->k * 8;
+  void* h = c->ring.reserve(bytes, c->stream);
+  memcpy(h, gates, bytes);
+  HIPCHK(hipMemcpyAsync(set->d_gates, h, bytes, hipMemcpyHostToDevice, c->stream));
 }
 
 // k experts per projection. Expert x of projection j has A = a[j * k + x],
 // B = b[j * k + x] and gate weight gates[j * k + x]; gates == nullptr (k == 1)
 // is a plain LoRA set.
 // Each packed batch holds, per expert, the gate-scaled A rows; the k encoded
-// plaintexts of a batch are folded into one (launch_pt_sum), which makes the
+// plaintexts of a batch are folded into one (queue_regate), which makes the
 // batch's product the ct_add of the k experts' products, bit for bit. The
 // B side applies sum_x g_x B_x to the decrypted intermediate.
 void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, const uint32_t* d_out,
@@ -1944,12 +1969,19 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->n_deltas = out_off;
   const uint32_t nb = set->n_batches, ni = set->n_in;
   const bool gated = gates != nullptr;
+  const uint32_t Lr = L > 1 ? L - 1 : 1;
+  // decrypt branch (ciphertext.rs:351): CRT over limbs 0, 1 iff scale > 1.5 * 2^40 and >= 2 limbs
+  const double scale_n = kScale * kScale, scale_r = scale_n / (double)c->q[L - 1];
+  const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
+  const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
+  // rescaled products straight into segment sums (rescale_decrypt_kernel)
+  // where the decryption reads limb 0 and its transform can sum the segments
+  const bool fused_rd = L >= 2 && nl_r == 1 && segsum_in_transform(c, nb, cols);
   if (!gated) {
     set->bmix = const_cast<double*>(persist(set, bmat));
   } else {
     set->bexp = persist(set, bmat);
     set->bmix = (double*)set->alloc((size_t)boff * 8);
-    set->d_moe_b = persist(set, moe_b);
     set->d_moe_p = persist(set, moe_p);
   }
   for (uint32_t j = 0; j < set->n_proj; ++j) bj[j].b = set->bmix + moe_p[j].off;
@@ -1991,8 +2023,28 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     HIPCHK(hipStreamSynchronize(c->stream));  // the scope's buffers return to the pool
   } else {
     set->apack = persist(set, packed);
+    set->moe_b = moe_b;
+    set->d_gates = (double*)set->alloc((size_t)set->n_proj * k * 8);
+    set->moe_m = (int64_t*)set->alloc((size_t)nb * k * N * 8);
+    // A token reads the plaintexts' limbs 0..nl-1 (its decryptions) and L-1
+    // (a rescale), in Montgomery form, and the plain form of limbs 0..nl_r-1
+    // only in a rescale on the split kernels (its store's ct x pt): the
+    // regated plaintexts are formed on those limbs.
+    const uint32_t nl_pt = std::max(nl_n, nl_r);
+    std::vector<NttJob> mj;
+    for (uint32_t bt = 0; bt < nb; ++bt)
+      for (uint32_t l = 0; l < L; ++l) {
+        if (l >= nl_pt && l != L - 1) continue;
+        const size_t off = ((size_t)bt * L + l) * N;
+        const bool plain = L >= 2 && !fused_rd && l < nl_r;
+        mj.push_back(NttJob{reinterpret_cast<const uint64_t*>(set->moe_m + (size_t)bt * k * N), set->ptm + off,
+                            plain ? set->pts + off : nullptr, nullptr, l, k});
+      }
+    set->d_moe_ntt = persist(set, mj);
+    set->moe_ntt_jobs = (uint32_t)mj.size();
+    upload_gates(set, gates);
     OpScope sc(c);
-    queue_regate(sc, set, sc.up(std::vector<double>(gates, gates + (size_t)set->n_proj * k)));
+    queue_regate(sc, set);
     HIPCHK(hipStreamSynchronize(c->stream));
   }
   // per-token job lists
@@ -2012,11 +2064,6 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   std::vector<NttJob> inv, fwd, dot_r, inv_nr;
   std::vector<RescaleDecryptJob> rd;
   std::vector<DecodeJob> dec_r(nb), dec_n(nb);
-  const uint32_t Lr = L > 1 ? L - 1 : 1;
-  // decrypt branch (ciphertext.rs:351): CRT over limbs 0, 1 iff scale > 1.5 * 2^40 and >= 2 limbs
-  const double scale_n = kScale * kScale, scale_r = scale_n / (double)c->q[L - 1];
-  const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
-  const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
   set->nl_n = nl_n;
   set->nl_r = nl_r;
   {
@@ -2057,9 +2104,6 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     std::tie(set->d_enc_r, set->enc_mask_r) = plan(((1u << nl_r) - 1) | (L >= 2 ? 1u << (L - 1) : 0u));
     std::tie(set->d_enc_n, set->enc_mask_n) = plan((1u << nl_n) - 1);
   }
-  // rescaled products straight into segment sums (rescale_decrypt_kernel)
-  // where the decryption reads limb 0 and its transform can sum the segments
-  const bool fused_rd = L >= 2 && nl_r == 1 && segsum_in_transform(c, nb, cols);
   if (!fused_rd) set->res = (uint64_t*)set->alloc(nb * 2 * nl_r * P);
   set->dkey = (uint64_t*)set->alloc((size_t)set->n_in * nl_n * P);
   for (uint32_t bt = 0; bt < nb; ++bt) {
@@ -2316,8 +2360,9 @@ int th_lora_set_gates(th_ctx* ctx, th_lora* set, const double* gates) {
     for (size_t i = 0; i < ng; ++i) need(std::isfinite(gates[i]), "gate weights must be finite");
     // a queued token redone later (sampler band) must see the plaintexts it was queued with
     if (!ctx->pending.empty()) drain(ctx);
+    upload_gates(set, gates);
     OpScope sc(ctx);
-    queue_regate(sc, set, sc.up(std::vector<double>(gates, gates + ng)));
+    queue_regate(sc, set);
   });
 }
 

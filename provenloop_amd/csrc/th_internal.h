@@ -22,6 +22,8 @@ namespace th {
 //            2: x = u mapped 0 -> q-1, 1 -> 0, 2 -> 1, src = u (u8)
 //   MULM     MUL with aux in Montgomery form (launch_to_montgomery); x in [0, 2q)
 //   DOTM     DOT with the key in Montgomery form; x in [0, 3q)
+//   MSUM     x = sum over e < job sub of (m_e[i] mod q) mod q, m_e = i64 coefficients
+//            at src + e N (the k experts' encoded vectors of a mixture batch)
 enum NttLoad : uint32_t {
   NTT_LOAD_NONE = 0,
   NTT_LOAD_MUL = 1,
@@ -29,7 +31,8 @@ enum NttLoad : uint32_t {
   NTT_LOAD_DOT = 3,
   NTT_LOAD_ENC = 4,
   NTT_LOAD_MULM = 5,
-  NTT_LOAD_DOTM = 6
+  NTT_LOAD_DOTM = 6,
+  NTT_LOAD_MSUM = 7
 };
 
 // Operation applied to every output of a FORWARD transform before it is
@@ -37,11 +40,19 @@ enum NttLoad : uint32_t {
 //   NONE         dst[i] = y
 //   RESCALE      dst[i] = (aux[i] - y) * q_last^{-1} mod q
 //   MUL_RESCALE  dst[i] = (aux[i] * aux2[i] - y) * q_last^{-1} mod q
-// With y = NTT_q(c_last mod q) these are the rescale of ciphertext.rs:476-535
-// in the evaluation domain: the NTT is linear mod q, so
+//   MONT         dst[i] = y 2^64 mod q (Montgomery form), and aux[i] = y when the
+//                job's aux is not null (aux is then written, not read)
+// With y = NTT_q(c_last mod q) the rescale forms are the rescale of
+// ciphertext.rs:476-535 in the evaluation domain: the NTT is linear mod q, so
 //   NTT_q((c_q - (c_last mod q)) * inv) = (C_q - NTT_q(c_last mod q)) * inv
 // for the limb's evaluation-domain input C_q (aux, or the product aux * aux2).
-enum NttStore : uint32_t { NTT_STORE_NONE = 0, NTT_STORE_RESCALE = 1, NTT_STORE_MUL_RESCALE = 2, NTT_STORE_SEGSUM = 3 };
+enum NttStore : uint32_t {
+  NTT_STORE_NONE = 0,
+  NTT_STORE_RESCALE = 1,
+  NTT_STORE_MUL_RESCALE = 2,
+  NTT_STORE_SEGSUM = 3,
+  NTT_STORE_MONT = 4
+};
 // NTT_STORE_SEGSUM (inverse, whole-polynomial kernel, limb 0 only): instead of
 // storing the decrypted coefficients m, the transform writes the ZeRo-MOAI
 // segment sums seg[c] = (sum_j v_j W_c[j]) / scale, v_j = m_j centred against
