@@ -138,14 +138,20 @@ __device__ __forceinline__ int64_t round_sat_i64(double x) {
   return (int64_t)r;
 }
 
+// m_j from FFT output a at position j (encoding.rs:186-204).
+__device__ __forceinline__ int64_t encoded_m(Cx a, uint32_t j, double inv_n, const double* __restrict__ twist_re,
+                                             const double* __restrict__ twist_im) {
+  const double a_re = a.re * inv_n;
+  const double a_im = a.im * inv_n;
+  const double coeff = a_re * twist_re[j] + a_im * twist_im[j];
+  return round_sat_i64(coeff * 1099511627776.0);  // * 2^40 (params.rs:12)
+}
+
 __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const BarrettConst* __restrict__ bc,
                                                  const double* __restrict__ twist_re,
                                                  const double* __restrict__ twist_im, uint32_t j, Cx a,
                                                  double inv_n, uint32_t n, uint32_t L) {
-  const double a_re = a.re * inv_n;
-  const double a_im = a.im * inv_n;
-  const double coeff = a_re * twist_re[j] + a_im * twist_im[j];
-  const int64_t m = round_sat_i64(coeff * 1099511627776.0);  // * 2^40 (params.rs:12)
+  const int64_t m = encoded_m(a, j, inv_n, twist_re, twist_im);
   if (jb.mvals) {
     gst(jb.mvals)[j] = m;
     return;
@@ -160,6 +166,25 @@ __device__ __forceinline__ void emit_coefficient(const EncodeJob& jb, const Barr
     dst[(size_t)l * n + j] = jb.e0 ? csub(mm + signed_residue_dev(e0, c), c.q) : mm;
     if (jb.e1) dst[(size_t)(L + l) * n + j] = signed_residue_dev(e1, c);
     if (jb.u) dst[(size_t)(2 * L + l) * n + j] = u == 0 ? c.q - 1 : (u == 1 ? 0 : 1);
+  }
+}
+
+// The FFT outputs at positions p*M + k of all P parts (x[p]), from the parts' stage-lb values.
+template <int LP>
+__device__ __forceinline__ void combine_parts(GPtr<double> Pd, uint32_t k, uint32_t M, GPtr<double> wr,
+                                              GPtr<double> wi, Cx (&x)[1 << LP]) {
+  constexpr int P = 1 << LP;
+#pragma unroll
+  for (int p = 0; p < P; ++p) x[p] = Cx{Pd[(size_t)p * 2 * M + k], Pd[(size_t)p * 2 * M + M + k]};
+#pragma unroll
+  for (int t = 0; t < LP; ++t) {
+    const uint32_t half = M << t;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (p & (1 << t)) continue;
+      const uint32_t w = half - 1 + (uint32_t)(p & ((1 << t) - 1)) * M + k;
+      dit(x[p], x[p | (1 << t)], wr[w], wi[w], x[p], x[p | (1 << t)]);
+    }
   }
 }
 
@@ -189,18 +214,7 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < G * M; i += gridDim.x * blockDim.x) {
     const uint32_t o = i >> lb, k = i & (M - 1);  // o is uniform over a wavefront (M >= 64)
     Cx x[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) x[p] = Cx{Pd[(size_t)p * 2 * M + k], Pd[(size_t)p * 2 * M + M + k]};
-#pragma unroll
-    for (int t = 0; t < LP; ++t) {
-      const uint32_t half = M << t;
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        if (p & (1 << t)) continue;
-        const uint32_t w = half - 1 + (uint32_t)(p & ((1 << t) - 1)) * M + k;
-        dit(x[p], x[p | (1 << t)], wr[w], wi[w], x[p], x[p | (1 << t)]);
-      }
-    }
+    combine_parts<LP>(Pd, k, M, wr, wi, x);
 #pragma unroll
     for (int s = 0; s < P / G; ++s) {
       Cx v = x[s * G];
@@ -212,21 +226,92 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
   }
 }
 
+// k_encode_final for groups of fold consecutive jobs (the experts of one
+// mixture batch) summed into one residue polynomial: group b writes, for each
+// limb l of limb_mask (at most ENC_FOLD_MAX_LIMBS of them), the sum over its
+// jobs x of (m_x mod q_l) mod q_l at jobs[b * fold].dst + l n: the residues
+// k_encode_final writes for each job (encoded_m, signed_residue_dev), summed.
+template <int LP>
+__global__ __launch_bounds__(256) void k_encode_final_fold(const EncodeJob* __restrict__ jobs, uint32_t fold,
+                                                           uint32_t limb_mask, const BarrettConst* __restrict__ bc,
+                                                           const double* __restrict__ twist_re,
+                                                           const double* __restrict__ twist_im,
+                                                           const double* __restrict__ stage_re,
+                                                           const double* __restrict__ stage_im, uint32_t logn) {
+  constexpr int P = 1 << LP;
+  constexpr int G = P >= 4 ? P / 4 : 1;
+  constexpr int C = P / G;  // coefficients per thread and job
+  constexpr int ML = ENC_FOLD_MAX_LIMBS;
+  const uint32_t n = 1u << logn, lb = logn - LP;
+  const uint32_t M = n >> LP;
+  const EncodeJob* grp = jobs + (size_t)blockIdx.y * fold;
+  uint32_t limb[ML];
+  uint32_t nl = 0;
+  for (uint32_t l = 0; l < 32 && nl < (uint32_t)ML; ++l)
+    if (limb_mask >> l & 1) limb[nl++] = l;
+  const GMut<uint64_t> dst = gst(grp[0].dst);
+  const GPtr<double> wr = gld(stage_re), wi = gld(stage_im);
+  const double inv_n = 1.0 / (double)n;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < G * M; i += gridDim.x * blockDim.x) {
+    const uint32_t o = i >> lb, k = i & (M - 1);  // o is uniform over a wavefront (M >= 64)
+    uint64_t acc[C][ML];
+#pragma unroll
+    for (int s = 0; s < C; ++s)
+#pragma unroll
+      for (int t = 0; t < ML; ++t) acc[s][t] = 0;
+    for (uint32_t e = 0; e < fold; ++e) {
+      Cx x[P];
+      combine_parts<LP>(gld(grp[e].parts), k, M, wr, wi, x);
+#pragma unroll
+      for (int s = 0; s < C; ++s) {
+        Cx v = x[s * G];
+#pragma unroll
+        for (int g = 1; g < G; ++g)
+          if (o == (uint32_t)g) v = x[s * G + g];
+        const uint32_t j = (uint32_t)(s * G) * M + o * M + k;
+        const int64_t m = encoded_m(v, j, inv_n, twist_re, twist_im);
+#pragma unroll
+        for (int t = 0; t < ML; ++t) {
+          if (t >= (int)nl) break;
+          const BarrettConst c = bc[limb[t]];
+          acc[s][t] = addmod(acc[s][t], signed_residue_dev(m, c), c.q);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < C; ++s) {
+      const uint32_t j = (uint32_t)(s * G) * M + o * M + k;
+#pragma unroll
+      for (int t = 0; t < ML; ++t) {
+        if (t >= (int)nl) break;
+        dst[(size_t)limb[t] * n + j] = acc[s][t];
+      }
+    }
+  }
+}
+
 size_t encode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base, const SampleJob* fix, const uint64_t* seeds,
-                         int force_serial, BandArgs band) {
+                         int force_serial, BandArgs band, uint32_t fold, uint32_t fold_limbs) {
   if (!njobs) return hipSuccess;
   if (fix && njobs > SEEDS_PER_LAUNCH) return hipErrorInvalidValue;
+  if (fold && (njobs % fold || !fold_limbs || __builtin_popcount(fold_limbs) > (int)ENC_FOLD_MAX_LIMBS ||
+               (L < 32 && fold_limbs >> L)))
+    return hipErrorInvalidValue;
   SeedBlock sb{};
   if (fix && seeds)
     for (uint32_t i = 0; i < njobs; ++i) sb.v[i] = seeds[i];
-  // at least one part per LDS budget; more parts (up to 16, of at least 1024
-  // values) while the batch would leave CUs idle: the parts are independent
+  // parts of at most 4096 values (two workgroups' LDS per CU; with 672
+  // encodes of N=16384 per CryptoMOE token, the token measured 0.656 ms with
+  // 4096-value parts against 0.697 ms with 8192, 0.675 ms with 2048 and
+  // 0.727 ms with 1024); more parts (up to 16, of at least 1024 values)
+  // while the batch would leave CUs idle: the parts are independent
   // workgroups and the result is the same for any split
-  uint32_t lp = fft_parts_log(logn);
+  const uint32_t lp_min = fft_parts_log(logn);
+  uint32_t lp = logn > 12 && logn - 12 > lp_min ? logn - 12 : lp_min;
   while (lp < 4 && logn - lp > 10 && njobs * (1u << lp) < 512) ++lp;
   const uint32_t M = (1u << logn) >> lp;
   // padded values (+ twiddles with 8 or more parts)
@@ -242,8 +327,12 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
     if (e != hipSuccess) return e;                                                                         \
     hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
                        stage_im, logn, z_base, fix, sb, (int)(seeds != nullptr), force_serial, band);     \
-    hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im, \
-                       stage_re, stage_im, logn, L);                                                       \
+    if (fold)                                                                                              \
+      hipLaunchKernelGGL(k_encode_final_fold<LP>, dim3(gx, njobs / fold), dim3(256), 0, s, jobs, fold,     \
+                         fold_limbs, bc, twist_re, twist_im, stage_re, stage_im, logn);                    \
+    else                                                                                                   \
+      hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re,         \
+                         twist_im, stage_re, stage_im, logn, L);                                           \
     return hipGetLastError();
   switch (lp) {
     TH_ENC(0)

@@ -13,7 +13,7 @@ struct EncodeJob {
   const int64_t* e1;   // rounded Gaussian e1, or null
   uint64_t* dst;       // [M (L) | E1 (L) | U (L)] limb-polys; only M when e1/u are null
   int64_t* mvals;      // non-null: write m itself (N i64) instead of dst (the residues are then
-                       // formed by the transforms' loads, NTT_LOAD_ENC or NTT_LOAD_MSUM)
+                       // formed by the encrypt transforms' loads, NTT_LOAD_ENC)
   double* parts;       // scratch, encode_parts_doubles(logn) doubles
   const double* gate;  // non-null (no replication): slots are gate[0] * z[slot] for slot < n_valid,
                        // 0 beyond (a gated expert's packed rows, inference_engine.py:1300-1308)
@@ -42,11 +42,17 @@ constexpr double SAMPLER_BAND_DEFAULT = 0x1p-36;
 // replication) instead of its z field. With fix (the sample jobs of a
 // flagged launch_sample_pk queued just before with fix_later, one per encode
 // job, at most SEEDS_PER_LAUNCH of them, and the same seeds), the launch also
-// finishes the sampler's rejection handling (k_sample_fix's work).
+// finishes the sampler's rejection handling (k_sample_fix's work). With fold
+// > 0, every fold consecutive jobs are summed into one residue polynomial
+// (the experts of a mixture batch): the group's first job's dst receives, on
+// the limbs in fold_limbs (at most ENC_FOLD_MAX_LIMBS), the sum mod q_l of
+// the residues each job would write; the jobs' other outputs are unused.
+constexpr uint32_t ENC_FOLD_MAX_LIMBS = 4;
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
                          uint32_t L, hipStream_t s, const double* z_base = nullptr, const SampleJob* fix = nullptr,
-                         const uint64_t* seeds = nullptr, int force_serial = 0, BandArgs band = BandArgs{nullptr, 0.0});
+                         const uint64_t* seeds = nullptr, int force_serial = 0, BandArgs band = BandArgs{nullptr, 0.0},
+                         uint32_t fold = 0, uint32_t fold_limbs = 0);
 size_t encode_parts_doubles(uint32_t logn);
 
 struct SampleJob {

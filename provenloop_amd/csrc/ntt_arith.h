@@ -96,9 +96,8 @@ struct LoadOp {
   const uint64_t* key;  // secret-key limb-poly (DOT)
   BarrettConst bc;
   RescaleConst rc;
-  uint32_t sub;         // ENC variant, MSUM vector count (uniform over the job)
-  uint32_t n;           // transform size (MSUM: stride of the vectors)
-  double qd, qinv;      // q and 1/q as doubles (ENC, MSUM)
+  uint32_t sub;         // ENC variant (uniform over the job)
+  double qd, qinv;      // q and 1/q as doubles (ENC)
   // signed_residue_dev with |e| in [q, 2^53) reduced by one exact FP64 step:
   // quot = rint(|e| / q) is within one of the true quotient, and the remainder
   // fma(-quot, q, |e|) is an exact integer in (-q, q)
@@ -171,12 +170,6 @@ struct LoadOp {
   }
   __device__ __forceinline__ uint64_t operator()(const uint64_t* src, uint32_t i) const {
     if constexpr (LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM) return finish(fetch(src, i));
-    if constexpr (LD == NTT_LOAD_MSUM) {
-      const GPtr<int64_t> m = gld(reinterpret_cast<const int64_t*>(src));
-      uint64_t acc = 0;
-      for (uint32_t e = 0; e < sub; ++e) acc = addmod(acc, enc_residue(m[(size_t)e * n + i]), bc.q);
-      return acc;
-    }
     const uint64_t x = gld(src)[i];
     if constexpr (LD == NTT_LOAD_DOTM) return x + mont_mul(gld(aux)[i], gld(key)[i], bc);
     if constexpr (LD == NTT_LOAD_MUL) return mulmod_barrett(x, gld(aux)[i], bc);
@@ -273,11 +266,10 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
                                         LoadOp<LD>& op, StoreOp<ST>& so) {
   op.aux = jb.aux;
   if constexpr (LD == NTT_LOAD_MUL || LD == NTT_LOAD_DOT || LD == NTT_LOAD_ENC || LD == NTT_LOAD_MULM ||
-                LD == NTT_LOAD_DOTM || LD == NTT_LOAD_MSUM)
+                LD == NTT_LOAD_DOTM)
     op.bc = a.bc[limb];
-  if constexpr (LD == NTT_LOAD_ENC || LD == NTT_LOAD_MSUM) {
+  if constexpr (LD == NTT_LOAD_ENC) {
     op.sub = jb.sub;
-    op.n = n;
     op.qd = a.lc[limb].qd;
     op.qinv = a.lc[limb].qinv;
   }
@@ -297,7 +289,7 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE | ENC,
-// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE), (MSUM, MONT); inverse
+// NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE), (NONE, MONT); inverse
 // (NONE | MUL | MULM | DOT, NONE), (DOT | DOTM, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
@@ -308,7 +300,7 @@ __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_RESCALE>();
     if (load == NTT_LOAD_REDUCE && store == NTT_STORE_MUL_RESCALE)
       return f.template operator()<NTT_LOAD_REDUCE, NTT_STORE_MUL_RESCALE>();
-    if (load == NTT_LOAD_MSUM && store == NTT_STORE_MONT) return f.template operator()<NTT_LOAD_MSUM, NTT_STORE_MONT>();
+    if (load == NTT_LOAD_NONE && store == NTT_STORE_MONT) return f.template operator()<NTT_LOAD_NONE, NTT_STORE_MONT>();
     return hipErrorInvalidValue;
   } else {
     if (load == NTT_LOAD_DOT && store == NTT_STORE_SEGSUM)

@@ -304,8 +304,8 @@ struct th_lora {
   uint32_t max_b_count = 0;
   std::vector<MoeBatch> moe_b;     // per batch: projection and rows (host copy)
   double* d_gates = nullptr;       // n_proj x k, the current gates
-  int64_t* moe_m = nullptr;        // n_batches x k x N: the experts' encoded vectors m
-  const NttJob* d_moe_ntt = nullptr;  // per batch and plaintext limb: sum of the k m, transform, Montgomery copy
+  uint32_t moe_limbs = 0;          // the plaintext limbs a token reads (bit l: limb l)
+  const NttJob* d_moe_ntt = nullptr;  // per batch and such limb: transform in place, Montgomery copy
   uint32_t moe_ntt_jobs = 0;
   // pinned host staging of host-I/O tokens (hidden states in, deltas and
   // segment sums out), the same pages every token
@@ -1875,15 +1875,15 @@ void launch_jobs_ntt(th_ctx* c, bool inverse, const NttJob* jobs, uint32_t n, Nt
 // n_proj x k): every batch's plaintext is sum_x encode_to_ntt(g_x * A_x rows)
 // (the encoder and transforms of th_encode_to_ntt), in Montgomery form (and
 // plain where a token reads it), and B = sum_x g_x B_x. The encoder gates the
-// experts' packed rows as it reads them and writes each vector's m (i64); the
-// forward transform of each batch and plaintext limb sums the k residues
-// m_x mod q_l in its loads (NTT_LOAD_MSUM) and writes the Montgomery form in
-// its store (NTT_STORE_MONT). The transform is linear mod q_l, so this is the
-// sum of the k transforms, residue by residue. Only the limbs a token reads
-// are formed (set->d_moe_ntt).
+// experts' packed rows as it reads them, and its last launch sums the k
+// experts' residues of each batch (the k encoded residue polynomials summed
+// mod q_l); each batch's forward transform then runs once per limb, in place,
+// and writes the Montgomery form in its store (NTT_STORE_MONT). The
+// transform is linear mod q_l, so this is the sum of the k transforms,
+// residue by residue. Only the limbs a token reads are formed.
 void queue_regate(OpScope& sc, th_lora* set) {
   th_ctx* c = sc.c;
-  const uint32_t N = c->N, S = N / 2, nb = set->n_batches, k = set->k;
+  const uint32_t N = c->N, S = N / 2, L = c->L, nb = set->n_batches, k = set->k;
   const size_t nv = (size_t)nb * k, pd = encode_parts_doubles(c->logn);
   double* parts = (double*)sc.dev(nv * pd * 8);
   std::vector<EncodeJob> ej(nv);
@@ -1892,12 +1892,13 @@ void queue_regate(OpScope& sc, th_lora* set) {
     ej[v].z = set->apack + v * S;
     ej[v].gate = set->d_gates + (size_t)mb.proj * k + v % k;
     ej[v].n_valid = mb.n_valid;
-    ej[v].mvals = set->moe_m + v * N;
+    ej[v].dst = set->ptm + (v / k) * L * N;  // the group's sums, transformed in place below
     ej[v].parts = parts + v * pd;
   }
   HIPCHK(launch_encode(sc.up(ej), (uint32_t)nv, c->d_bc, c->d_twist_re, c->d_twist_im, c->d_stage_re, c->d_stage_im,
-                       c->logn, c->L, c->stream));
-  launch_jobs_ntt(c, false, set->d_moe_ntt, set->moe_ntt_jobs, NTT_LOAD_MSUM, nullptr, nullptr, NTT_STORE_MONT);
+                       c->logn, L, c->stream, nullptr, nullptr, nullptr, 0, BandArgs{nullptr, 0.0}, k,
+                       set->moe_limbs));
+  launch_jobs_ntt(c, false, set->d_moe_ntt, set->moe_ntt_jobs, NTT_LOAD_NONE, nullptr, nullptr, NTT_STORE_MONT);
   HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, set->d_gates, set->n_proj, k, set->max_b_count, set->bmix,
                           c->stream));
 }
@@ -2025,20 +2026,19 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->apack = persist(set, packed);
     set->moe_b = moe_b;
     set->d_gates = (double*)set->alloc((size_t)set->n_proj * k * 8);
-    set->moe_m = (int64_t*)set->alloc((size_t)nb * k * N * 8);
     // A token reads the plaintexts' limbs 0..nl-1 (its decryptions) and L-1
     // (a rescale), in Montgomery form, and the plain form of limbs 0..nl_r-1
     // only in a rescale on the split kernels (its store's ct x pt): the
     // regated plaintexts are formed on those limbs.
     const uint32_t nl_pt = std::max(nl_n, nl_r);
+    set->moe_limbs = ((1u << nl_pt) - 1) | (1u << (L - 1));
     std::vector<NttJob> mj;
     for (uint32_t bt = 0; bt < nb; ++bt)
       for (uint32_t l = 0; l < L; ++l) {
-        if (l >= nl_pt && l != L - 1) continue;
+        if (!(set->moe_limbs >> l & 1)) continue;
         const size_t off = ((size_t)bt * L + l) * N;
         const bool plain = L >= 2 && !fused_rd && l < nl_r;
-        mj.push_back(NttJob{reinterpret_cast<const uint64_t*>(set->moe_m + (size_t)bt * k * N), set->ptm + off,
-                            plain ? set->pts + off : nullptr, nullptr, l, k});
+        mj.push_back(NttJob{set->ptm + off, set->ptm + off, plain ? set->pts + off : nullptr, nullptr, l, 0});
       }
     set->d_moe_ntt = persist(set, mj);
     set->moe_ntt_jobs = (uint32_t)mj.size();

@@ -22,8 +22,6 @@ namespace th {
 //            2: x = u mapped 0 -> q-1, 1 -> 0, 2 -> 1, src = u (u8)
 //   MULM     MUL with aux in Montgomery form (launch_to_montgomery); x in [0, 2q)
 //   DOTM     DOT with the key in Montgomery form; x in [0, 3q)
-//   MSUM     x = sum over e < job sub of (m_e[i] mod q) mod q, m_e = i64 coefficients
-//            at src + e N (the k experts' encoded vectors of a mixture batch)
 enum NttLoad : uint32_t {
   NTT_LOAD_NONE = 0,
   NTT_LOAD_MUL = 1,
@@ -31,8 +29,7 @@ enum NttLoad : uint32_t {
   NTT_LOAD_DOT = 3,
   NTT_LOAD_ENC = 4,
   NTT_LOAD_MULM = 5,
-  NTT_LOAD_DOTM = 6,
-  NTT_LOAD_MSUM = 7
+  NTT_LOAD_DOTM = 6
 };
 
 // Operation applied to every output of a FORWARD transform before it is
