@@ -203,7 +203,7 @@ struct StoreOp {
                                         uint64_t cp) const {
     if constexpr (ST == NTT_STORE_MONT) {
       const uint64_t y = ar.fwd_store(x);
-      dst[i] = mulmod_barrett(y, bc.r64, bc);
+      dst[i] = csub(shoup_lazy(y, bc.r64, bc.r64_s, bc.q), bc.q);  // y 2^64 mod q
       if (aux) gst(const_cast<uint64_t*>(aux))[i] = y;
     } else {
       dst[i] = apply_prep(ar, x, cp);

@@ -81,7 +81,7 @@ __global__ void k_to_montgomery(const uint64_t* __restrict__ src, uint64_t* __re
                                 const BarrettConst* __restrict__ bc, uint32_t n, uint32_t L, uint64_t total) {
   for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
     const BarrettConst& m = bc[(e / n) % L];
-    dst[e] = mulmod_barrett(src[e], m.r64, m);
+    dst[e] = csub(shoup_lazy(src[e], m.r64, m.r64_s, m.q), m.q);
   }
 }
 

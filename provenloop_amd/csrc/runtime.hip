@@ -634,7 +634,8 @@ void build_tables(th_ctx* c) {
     const u128 r = (~(u128)0) / q;
     uint64_t qi = 1;  // q^{-1} mod 2^64 by Newton's iteration (each step doubles the correct bits)
     for (int it = 0; it < 6; ++it) qi *= 2 - q * qi;
-    bc[l] = BarrettConst{q, (uint64_t)(r >> 64), (uint64_t)r, (uint64_t)0 - qi, (uint64_t)(((u128)1 << 64) % q)};
+    const uint64_t r64 = (uint64_t)(((u128)1 << 64) % q);
+    bc[l] = BarrettConst{q, (uint64_t)(r >> 64), (uint64_t)r, (uint64_t)0 - qi, r64, (uint64_t)(((u128)r64 << 64) / q)};
   }
   HIPCHK(hipMemcpy(c->d_tables, host_tab.data(), tab_bytes, hipMemcpyHostToDevice));
   HIPCHK(hipMalloc(&c->d_lc, L * sizeof(LimbConst)));

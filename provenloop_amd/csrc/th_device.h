@@ -142,6 +142,7 @@ struct BarrettConst {
   uint64_t r_hi, r_lo;  // floor((2^128 - 1) / q) as two words
   uint64_t mq;          // -q^{-1} mod 2^64 (Montgomery products)
   uint64_t r64;         // 2^64 mod q (into Montgomery form)
+  uint64_t r64_s;       // floor(r64 2^64 / q): its Shoup companion
 };
 
 __device__ __forceinline__ uint64_t mulmod_barrett(uint64_t a, uint64_t b, const BarrettConst& m) {
