@@ -5,17 +5,20 @@ Step = one per-token HE-LoRA pass at Qwen2.5-1.5B shape, N = 16384, the
 reference's 4-limb chain, scale 2^40: 28 layers x {q, v} projections
 (hidden 1536, rank 16, B_q [1536,16], B_v [256,16]). Per token: 28
 encrypt_pk of the replicated layer inputs, 224 column-packed ct x pt
-products (4 batches per projection), 224 rescales, one batched GPU decrypt
-with segment sums, then B @ intermediate, all on the GPU (one LoRA-set
-call, one stream synchronisation). Hidden states are in HBM before the
-timed region starts and the deltas stay in HBM; the same pass with host
+products (4 batches per projection), each rescaled and decrypted with
+segment sums, then B @ intermediate, all on the GPU (one LoRA-set call, one
+stream synchronisation; the pass forms the limbs its decryptions read, and
+its deltas are those of the full sequence). Hidden states are in HBM before
+the timed region starts and the deltas stay in HBM; the same pass with host
 inputs and outputs is reported beside it as pcie_inclusive. 56 encrypted
-LoRA deltas per token; value = deltas/s.
+LoRA deltas per token; value = deltas/s. Order on the GPU: the roofline
+microbench, the warm-up tokens, the pipelined and the reference-sequence
+tokens, the timed tokens, the host-I/O tokens, then the other figures.
 
 Also measured in the same run:
   * roofline: the batched NTT (64 polynomials x 4 limbs, N = 16384, forward
     and inverse as separate launches), timed with HIP events on the engine's
-    stream right before the token pass; algorithmic bytes = read + write of
+    stream before the token passes; algorithmic bytes = read + write of
     every limb-polynomial; the same round trip at N = 32768 (reference chain
     for that degree) is reported beside it as ntt_n32768;
   * single_delta: the latency of one encrypted LoRA delta (encrypt_pk, 4
@@ -687,15 +690,34 @@ def main():
     seed_arr = {t: np.asarray(seeds[t], np.uint64) for t in range(args.steps)}  # prepared like the inputs
     warm_seeds = [np.asarray(seeds_for(t), np.uint64) for t in warm]
     ntt16 = NttRoofline(ctx)
-    # The roofline microbench runs right before the token pass: after an idle
-    # period the GPU's clocks ramp up over some tens of ms of load (a
-    # power-management state that returns after every idle second, not
-    # one-time set-up), and its ~50 ms of launches keep the device busy up to
-    # the first warm-up token.
+    # Order: the roofline microbench, the warm-up tokens, the pipelined and the
+    # reference-sequence figures, then the timed synchronised tokens. After
+    # an idle second (or a host-bound stretch such as building a LoRA set) a
+    # synchronised token runs up to 8 % slower for about its first 100
+    # tokens (the GPU's clocks ramp under load; a power-management state,
+    # not set-up: it returns after every idle second); the measurements
+    # before the timed tokens keep the device busy up to them.
     ntt16.time(reps=60)
     for w in range(args.warmup):
         dev.run(pk, sk, args.steps + w, warm_seeds[w])
     ctx.sync()
+
+    # the same tokens queued back to back (host launches overlap the GPU; one sync at the end)
+    t2 = time.perf_counter()
+    for t in range(args.steps):
+        dev.run(pk, sk, t, seed_arr[t])
+    ctx.sync()
+    piped = time.perf_counter() - t2
+
+    # the reference's own call sequence: ct x pt, then decrypt without a rescale
+    # (inference_engine.py:1311-1315; the CRT branch of ciphertext.rs:351-396)
+    t3 = time.perf_counter()
+    for t in range(args.steps):
+        dev.run(pk, sk, t, seed_arr[t], rescale=False)
+        ctx.sync()
+    norescale_elapsed = time.perf_counter() - t3
+    flat_nr = dev.deltas(args.steps - 1)
+
     tok = []
     t0 = time.perf_counter()
     for t in range(args.steps):
@@ -707,31 +729,15 @@ def main():
     value = deltas_per_token * args.steps / elapsed
     tok_ms = np.diff(np.concatenate([[t0], tok])) * 1e3
 
-    # the same tokens queued back to back (host launches overlap the GPU; one sync at the end)
-    t2 = time.perf_counter()
-    for t in range(args.steps):
-        dev.run(pk, sk, t, seed_arr[t])
-    ctx.sync()
-    piped = time.perf_counter() - t2
-
     # the same pass with host inputs and outputs (PCIe included): reported beside value
     t1 = time.perf_counter()
     for t in range(args.steps):
         host_out = lora.deltas(pk, sk, np.stack(hidden[t]), seeds[t])
     pcie_elapsed = time.perf_counter() - t1
 
-    # the reference's own call sequence: ct x pt, then decrypt without a rescale
-    # (inference_engine.py:1311-1315; the CRT branch of ciphertext.rs:351-396)
-    t3 = time.perf_counter()
-    for t in range(args.steps):
-        dev.run(pk, sk, t, seed_arr[t], rescale=False)
-        ctx.sync()
-    norescale_elapsed = time.perf_counter() - t3
-    flat_nr = dev.deltas(args.steps - 1)
-
     # parity on layers 0 and 27 of token steps-1 against the oracle (the
-    # device outputs of the rescaled pass were overwritten by the pass without
-    # rescale; the host-I/O pass left the same token's deltas in host_out)
+    # host-I/O pass left that token's deltas in host_out; the device-I/O run of
+    # the same token is compared with them)
     last = args.steps - 1
     flat = np.concatenate(host_out)
     dev.run(pk, sk, last, seed_arr[last])
