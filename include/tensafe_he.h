@@ -98,8 +98,12 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
  *   the next th_ctx_sync, th_memcpy_d2h, th_lora_free or synchronising call,
  *   which queues a flagged token again (and, in order, the tokens queued after
  *   it) before returning. A wider band only makes the host redraw more often
- *   (tests use it to exercise that path). */
-enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2, TH_OPT_SAMPLER_BAND = 3 };
+ *   (tests use it to exercise that path).
+ * TH_OPT_SPLIT_RESCALE_DECRYPT: 1 makes LoRA sets created afterwards rescale
+ *   and decrypt their products on the split kernels also where one
+ *   workgroup per product would serve (N <= 16384, at most 256 batches);
+ *   the results are the same bit for bit; testing and measurement only. */
+enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2, TH_OPT_SAMPLER_BAND = 3, TH_OPT_SPLIT_RESCALE_DECRYPT = 4 };
 enum { TH_SAMPLER_DEVICE = 0, TH_SAMPLER_HOST = 1 };
 int th_ctx_set_option(th_ctx* ctx, int option, int64_t value);
 /* Counters of the context (no counterpart in the reference): the number of

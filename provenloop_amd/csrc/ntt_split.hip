@@ -631,4 +631,238 @@ hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t n
   }
 }
 
+// ------------------------------------------------------------------ rescale-decrypt, split sizes
+// The rescale and decryption of a LoRA set's products on limb 0 (the
+// algebra of rescale_decrypt_kernel, ntt.hip) in four launches of
+// single-wavefront workgroups, for sizes and batch counts the
+// whole-polynomial kernel does not serve. Per batch, with X, Y the last limb
+// of c0 pt, c1 pt:
+//   1. inverse row passes of X and Y with ct x pt in the loads
+//      (ntt_split_kernel, NTT_LOAD_MULM);
+//   2. rd_column_kernel: inverse column passes; X's canonical coefficients
+//      are reduced mod q0 (r0) and written in place, Y's reduced mod q0 and
+//      carried through the forward column pass at q0;
+//   3. rd_row_kernel: forward row pass of r1, D pt - NTT(r1) s in
+//      registers, inverse row pass (the same 1024 coefficients of a row);
+//   4. rd_column_sums_kernel: inverse column pass, (m - r0) inv mod q0,
+//      centred, and each lane's partial segment sums;
+//   5. rd_sums_final_kernel: the partial sums of each batch added up.
+// Lane l of column part p holds coefficients t + k 2^(LOGN-4), k = 0..15,
+// with t = (row << CB) | col (ColumnMap, Q1), the elements thread t holds
+// in the whole-polynomial kernel's epilogue at N = 16384; its partial sums
+// run over k in the same order, and step 5 adds them as that epilogue does
+// (a butterfly tree over 64 consecutive t, then the trees in order), so the
+// sums are bit-identical to rescale_decrypt_kernel's.
+
+// Step 2. Workgroup w: part w % PARTS of inverse job w / PARTS (jobs 2b, 2b+1
+// = X, Y of batch b; their dst holds step 1's intermediate).
+template <int LOGN>
+__global__ __launch_bounds__(64) void rd_column_kernel(NttArgs inv, const RescaleConst* __restrict__ rc0,
+                                                       const LimbConst* __restrict__ lc0p) {
+  using S = Split<LOGN>;
+  __shared__ uint64_t lds[S::LDS];
+  const uint32_t job = blockIdx.x / S::PARTS;
+  const ColumnMap<LOGN> m(column_part<LOGN>(blockIdx.x % S::PARTS));
+  const NttJob ij = inv.jobs[job];
+  const LimbConst& lci = inv.lc[ij.limb];
+  const RescaleConst rc = *rc0;
+  uint64_t c[16];  // the last limb's canonical coefficients, then reduced mod q0
+  if (lci.fp64) {
+    const Fp64Arith ar(lci);
+    Fp64Arith::V x[16];
+    column_inv_regs<LOGN>(x, ij.dst, lci, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
+  } else {
+    const IntArith ar(lci);
+    IntArith::V x[16];
+    column_inv_regs<LOGN>(x, ij.dst, lci, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) c[k] = c[k] < rc.q ? c[k] : mulmod_barrett(c[k], 1, rc.b);
+  if ((job & 1) == 0) {
+    const GMut<uint64_t> out = gst(ij.dst);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) out[m.j1(k)] = c[k];  // r0, natural order
+    return;
+  }
+  const LimbConst& lc0 = *lc0p;
+  if (lc0.fp64) {
+    const Fp64Arith ar(lc0);
+    Fp64Arith::V x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k]);
+    column_fwd_regs<LOGN, Fp64Arith, true>(x, ij.dst, lc0, m, ar, lds);
+  } else {
+    const IntArith ar(lc0);
+    IntArith::V x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = ar.load(c[k]);
+    column_fwd_regs<LOGN, IntArith, true>(x, ij.dst, lc0, m, ar, lds);
+  }
+}
+
+// Step 3. Workgroup w: part w % PARTS of batch w / PARTS (RescaleDecryptJob:
+// y holds step 2's forward column intermediate; rewritten in place with the
+// inverse row pass's intermediate of D pt - NTT(r1) s).
+template <int LOGN>
+__global__ __launch_bounds__(64) void rd_row_kernel(RescaleDecryptArgs a) {
+  using S = Split<LOGN>;
+  constexpr int CB = S::CB, M = (1 << (CB - 4)) - 1;
+  __shared__ uint64_t lds_raw[S::LDS];
+  const RescaleDecryptJob jb = a.jobs[blockIdx.x / S::PARTS];
+  const uint32_t part = blockIdx.x % S::PARTS;
+  const LimbConst& lc = a.lc[0];
+  const BarrettConst bc = *a.bc;
+  const uint32_t l = threadIdx.x;
+  const uint32_t jbase = part << 10;
+  const uint32_t rowbits = (l >> (CB - 4)) << CB;
+  auto p1 = [&](uint32_t k) { return (l & M) | (k << (CB - 4)) | rowbits; };
+  auto p2 = [&](uint32_t k) { return k | ((l & M) << 4) | rowbits; };
+  auto g = [&](uint32_t k) { return l + 64 * k; };
+  auto run = [&]<class A>() {
+    const A ar(lc);
+    typename A::V x[16];
+    typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+    row_fwd_regs<LOGN>(x, jb.y, lc, ar, part, lds_raw);
+    {
+      // D pt - NTT(r1) s at positions jbase + g(k): Montgomery products, each
+      // in [0, 2q), so the difference plus 2q is in (0, 4q), the integer
+      // inverse's input range; the FP64 inverse gets it canonical
+      const GPtr<uint64_t> d = gld(jb.d), p = gld(jb.ptm), sk = gld(a.skm);
+      const uint64_t q = lc.q, two_q = 2 * lc.q;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t i = jbase + g(k);
+        const uint64_t u = mont_mul(d[i], p[i], bc);
+        const uint64_t t = mont_mul(ar.fwd_store(x[k]), sk[i], bc);
+        uint64_t e = u + two_q - t;
+        if constexpr (std::is_same_v<A, Fp64Arith>) e = csub(csub(e, two_q), q);
+        x[k] = ar.load(e);
+      }
+    }
+    const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
+    wave_exchange(x, lds, g, p2);
+    inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+    wave_exchange(x, lds, p2, p1);
+    inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
+    const GMut<uint64_t> out = gst(const_cast<uint64_t*>(jb.y));
+#pragma unroll
+    for (int k = 0; k < 16; ++k) out[jbase + p1(k)] = ar.raw(x[k]);
+  };
+  if (lc.fp64)
+    run.template operator()<Fp64Arith>();
+  else
+    run.template operator()<IntArith>();
+}
+
+// Step 4. Workgroup w: column part w % PARTS of batch w / PARTS; writes
+// lane t's sums for segments c < cols at partials + (b cols + c) T + t,
+// T = 2^(LOGN-4).
+template <int LOGN>
+__global__ __launch_bounds__(64) void rd_column_sums_kernel(RescaleDecryptArgs a, double* __restrict__ partials) {
+  using S = Split<LOGN>;
+  constexpr int MAXC = NTT_SEGSUM_FUSED_MAX_COLS;
+  constexpr uint32_t T = 1u << (LOGN - 4);
+  __shared__ uint64_t lds[S::LDS];
+  const uint32_t b = blockIdx.x / S::PARTS;
+  const RescaleDecryptJob jb = a.jobs[b];
+  const ColumnMap<LOGN> m(column_part<LOGN>(blockIdx.x % S::PARTS));
+  const LimbConst& lc = a.lc[0];
+  const RescaleConst rc = *a.rc;
+  const uint64_t q = lc.q, half = q >> 1;
+  uint64_t mv[16];
+  if (lc.fp64) {
+    const Fp64Arith ar(lc);
+    Fp64Arith::V x[16];
+    column_inv_regs<LOGN>(x, jb.y, lc, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) mv[k] = ar.inv_store(x[k]);
+  } else {
+    const IntArith ar(lc);
+    IntArith::V x[16];
+    column_inv_regs<LOGN>(x, jb.y, lc, m, ar, lds);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) mv[k] = ar.inv_store(x[k]);
+  }
+  using D2 = double __attribute__((ext_vector_type(2)));
+  const GPtr<D2> W = gld(reinterpret_cast<const D2*>(a.segw));
+  const GPtr<uint64_t> r0 = gld(jb.x);
+  double acc[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t j = m.j1(k);
+    const uint64_t v0 = csub(shoup_lazy(submod(mv[k], r0[j], q), rc.inv, rc.inv_s, q), q);
+    const double v = v0 > half ? -(double)(q - v0) : (double)v0;
+    const D2 p = W[j];  // W_0[j], 2 cos(2 phi_j)
+    double wp = p.x, wc = p.x;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      if (c >= (int)a.cols) break;
+      acc[c] += v * wc;
+      const double wn = p.y * wc - wp;
+      wp = wc;
+      wc = wn;
+    }
+  }
+  const uint32_t t = m.j1(0);  // < T
+  const GMut<double> out = gst(partials) + (size_t)b * a.cols * T + t;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    if (c >= (int)a.cols) break;
+    out[(size_t)c * T] = acc[c];
+  }
+}
+
+// Step 5. One wavefront per batch: for each segment, the sum over groups of
+// 64 consecutive lanes t by a butterfly tree, the groups added in order.
+template <int LOGN>
+__global__ __launch_bounds__(64) void rd_sums_final_kernel(RescaleDecryptArgs a, const double* __restrict__ partials) {
+  constexpr uint32_t T = 1u << (LOGN - 4);
+  const uint32_t b = blockIdx.x, lane = threadIdx.x;
+  const RescaleDecryptJob jb = a.jobs[b];
+  const GPtr<double> in = gld(partials) + (size_t)b * a.cols * T;
+  for (uint32_t c = 0; c < a.cols; ++c) {
+    double t = 0.0;
+    for (uint32_t w = 0; w < T / 64; ++w) {
+      double v = in[(size_t)c * T + w * 64 + lane];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+      t += v;
+    }
+    if (lane == 0) gst(jb.seg)[c] = t / jb.scale;
+  }
+}
+
+template <int LOGN>
+static hipError_t launch_rd_split_t(const NttArgs& inv, const RescaleDecryptArgs& a, uint32_t nb, double* partials,
+                                    hipStream_t s) {
+  using S = Split<LOGN>;
+  const dim3 block(64);
+  hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, NTT_LOAD_MULM, NTT_STORE_NONE>), dim3(2 * nb * S::PARTS),
+                     block, 0, s, inv);
+  hipLaunchKernelGGL((rd_column_kernel<LOGN>), dim3(2 * nb * S::PARTS), block, 0, s, inv, a.rc, a.lc);
+  hipLaunchKernelGGL((rd_row_kernel<LOGN>), dim3(nb * S::PARTS), block, 0, s, a);
+  hipLaunchKernelGGL((rd_column_sums_kernel<LOGN>), dim3(nb * S::PARTS), block, 0, s, a, partials);
+  hipLaunchKernelGGL((rd_sums_final_kernel<LOGN>), dim3(nb), block, 0, s, a, (const double*)partials);
+  return hipGetLastError();
+}
+
+hipError_t launch_rescale_decrypt_split(int logn, const NttArgs& inv, const RescaleDecryptArgs& a, uint32_t nb,
+                                        double* partials, hipStream_t s) {
+  if (nb == 0) return hipSuccess;
+  if (!inv.jobs || inv.load != NTT_LOAD_MULM || a.cols < 1 || a.cols > NTT_SEGSUM_FUSED_MAX_COLS)
+    return hipErrorInvalidValue;
+  switch (logn) {
+    case 13: return launch_rd_split_t<13>(inv, a, nb, partials, s);
+    case 14: return launch_rd_split_t<14>(inv, a, nb, partials, s);
+    case 15: return launch_rd_split_t<15>(inv, a, nb, partials, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace th

@@ -211,6 +211,7 @@ struct th_ctx {
   int host_sampler = 0;   // TH_OPT_SAMPLER
   int force_serial = 0;   // TH_OPT_FORCE_SERIAL_SAMPLER
   double band = SAMPLER_BAND_DEFAULT;  // TH_OPT_SAMPLER_BAND
+  int split_rd = 0;       // TH_OPT_SPLIT_RESCALE_DECRYPT
   // Band flags of the device sampler (BandArgs): pinned host bytes the
   // kernels write through bflag_dev. A call takes a region of one byte per
   // sampled input (take_flags); asynchronous tokens keep theirs until the
@@ -282,8 +283,11 @@ struct th_lora {
   uint32_t enc_mask_r = 0, enc_mask_n = 0;
   const NttJob* d_dot_seg = nullptr;  // rescaled decrypts whose transform writes the segment sums
   // rescaled products decrypted on limb 0 straight from the last limb's
-  // inverse transforms (rescale_decrypt_kernel), one job per batch
+  // inverse transforms, one job per batch: rescale_decrypt_kernel, or the
+  // split kernels (rd_split, with nb x cols x N/16 doubles of partial sums)
   const RescaleDecryptJob* d_rd = nullptr;
+  bool rd_split = false;
+  double* rd_partials = nullptr;
   // decrypt without a rescale: D = c0 + c1 s per input (k_key_dot), then per
   // batch the inverse transforms of pt * D (the product's decryption)
   uint64_t* dkey = nullptr;           // n_in x nl x N
@@ -1503,6 +1507,9 @@ int th_ctx_set_option(th_ctx* ctx, int option, int64_t value) {
         need(value >= -52 && value <= -1, "sampler band must be 2^v for v in [-52, -1]");
         ctx->band = std::ldexp(1.0, (int)value);
         break;
+      case TH_OPT_SPLIT_RESCALE_DECRYPT:
+        ctx->split_rd = value != 0;
+        break;
       default:
         raise(TH_EINVAL, "unknown option " + std::to_string(option));
     }
@@ -1976,9 +1983,16 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const double scale_n = kScale * kScale, scale_r = scale_n / (double)c->q[L - 1];
   const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
-  // rescaled products straight into segment sums (rescale_decrypt_kernel)
-  // where the decryption reads limb 0 and its transform can sum the segments
-  const bool fused_rd = L >= 2 && nl_r == 1 && segsum_in_transform(c, nb, cols);
+  // rescaled products straight into segment sums where the decryption reads
+  // limb 0: one workgroup per product (rescale_decrypt_kernel) where its
+  // transform can sum the segments, else the split kernels
+  // (launch_rescale_decrypt_split)
+  const bool rd_ok = L >= 2 && nl_r == 1 && cols >= 1 && cols <= NTT_SEGSUM_FUSED_MAX_COLS;
+  const bool rd_whole = rd_ok && !c->split_rd && segsum_in_transform(c, nb, cols);
+  const bool rd_split = rd_ok && !rd_whole && c->logn >= 13;
+  const bool fused_rd = rd_whole || rd_split;
+  set->rd_split = rd_split;
+  if (rd_split) set->rd_partials = (double*)set->alloc((size_t)nb * cols * (N / 16) * 8);
   if (!gated) {
     set->bmix = const_cast<double*>(persist(set, bmat));
   } else {
@@ -2239,7 +2253,6 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     // the last limb of (c0 pt, c1 pt) as coefficients (ct x pt in the inverse
     // transforms' loads), D = c0 + c1 s on limb 0 per input, then each batch's
     // rescale and decryption on limb 0 in one kernel, which writes the sums
-    launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MULM);
     RescaleDecryptArgs ra{};
     ra.lc = ctx->d_lc;
     ra.bc = ctx->d_bc;
@@ -2248,7 +2261,17 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     ra.segw = set->seg_p;
     ra.jobs = set->d_rd;
     ra.cols = set->cols;
-    HIPCHK(launch_rescale_decrypt((int)ctx->logn, ra, nb, st));
+    if (set->rd_split) {
+      NttArgs ia{};
+      ia.lc = ctx->d_lc;
+      ia.bc = ctx->d_bc;
+      ia.jobs = set->d_inv_mul;
+      ia.load = NTT_LOAD_MULM;
+      HIPCHK(launch_rescale_decrypt_split((int)ctx->logn, ia, ra, nb, set->rd_partials, st));
+    } else {
+      launch_jobs_ntt(ctx, true, set->d_inv_mul, nb * 2, NTT_LOAD_MULM);
+      HIPCHK(launch_rescale_decrypt((int)ctx->logn, ra, nb, st));
+    }
   } else if (do_rescale) {
     // ct x pt inside the rescale's inverse transforms, rescale combine inside the forward ones
     NttArgs ia{}, fa{};

@@ -159,6 +159,14 @@ hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const Ntt
                           hipStream_t s);
 // njobs rescale_decrypt_kernel workgroups (whole-polynomial sizes, N <= 16384).
 hipError_t launch_rescale_decrypt(int logn, const RescaleDecryptArgs& a, uint32_t njobs, hipStream_t s);
+// The same for nb batches on the split kernels (N = 8192 .. 32768), from the
+// products' last limbs: inv = the 2 nb inverse jobs (X, Y of batch b at 2b,
+// 2b+1; src = ct's last limb, aux = pt's last limb in Montgomery form, load
+// NTT_LOAD_MULM, dst = the batch's x, y work areas); partials: scratch of
+// nb x cols x N/16 doubles. The segment sums equal launch_rescale_decrypt's
+// bit for bit at N = 16384.
+hipError_t launch_rescale_decrypt_split(int logn, const NttArgs& inv, const RescaleDecryptArgs& a, uint32_t nb,
+                                        double* partials, hipStream_t s);
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;

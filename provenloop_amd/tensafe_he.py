@@ -465,6 +465,11 @@ class CkksContext:
         _lib.check(_lib.load().th_ctx_stats(self._h, C.byref(v)))
         return v.value
 
+    def _split_rescale_decrypt(self, on: bool):
+        """Testing hook: LoRA sets created afterwards rescale and decrypt on the
+        split kernels also where one workgroup per product would serve."""
+        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_SPLIT_RESCALE_DECRYPT, int(on)))
+
     def _force_serial_sampler(self, on: bool):
         """Testing hook: replay every device stream serially (the rejection path)."""
         _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_FORCE_SERIAL_SAMPLER, int(on)))

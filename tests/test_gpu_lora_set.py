@@ -303,10 +303,11 @@ def test_lora_set_rescale_decrypt_chains(n, moduli, d):
 
 
 def test_lora_set_many_batches_rescale(env):
-    """260 batches, more than one round of whole-polynomial workgroups: the rescale of the limbs
-    the decryption reads runs on the split kernels and a separate decryption follows. The
-    segment sums equal th_lora_a_pass's bit for bit; the first two projections match the
-    oracle."""
+    """260 batches, more than one round of one-workgroup-per-product kernels: the rescale and
+    decryption run on the split kernels. A batch's sums depend only on its input, plaintext
+    and keys, so the first 256 batches equal, bit for bit, those of a set of the first 64
+    projections (one workgroup per product); all of them match th_lora_a_pass (which sums
+    the segments in another order) to 1e-12, and the first two projections the oracle."""
     eng, ref, sk, pk, rsk, rpk = env
     rng = np.random.default_rng(17)
     H = rng.normal(size=(2, 1536)) * 0.1
@@ -315,12 +316,70 @@ def test_lora_set_many_batches_rescale(env):
     assert ls.n_batches == 260
     seeds = [51, 52]
     got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=True, with_intermediates=True)
+    first = zero_moai.LoraSet(eng, 2, proj[:64])
+    assert first.n_batches == 256
+    f_got, f_sums = first.deltas(pk, sk, H, seeds, rescale=True, with_intermediates=True)
+    assert np.array_equal(f_sums, got_sums[:256])
+    assert all(np.array_equal(a, b) for a, b in zip(f_got, got[:64]))
     packs = [(i, zero_moai.pack_rows(A, 8192)) for i, A, _ in proj]
     pts = [eng.encode_to_ntt(p) for _, ps in packs for p in ps]
     pin = [i for i, ps in packs for _ in ps]
-    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=True), got_sums)
+    comp = eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=True)
+    assert np.max(np.abs(comp - got_sums)) <= 1e-12 * np.max(np.abs(comp))
     exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj[:2], True)
     _check(got[:2], got_sums[:8], exp, exp_sums)
+
+
+def test_lora_set_split_rescale_decrypt_equals_whole(env):
+    """The split-kernel rescale-decrypt (forced where one workgroup per product would serve)
+    gives the same segment sums and deltas, bit for bit, as the one-workgroup kernel and as
+    th_lora_a_pass, at the full token shape's 4 batches per projection."""
+    eng, ref, sk, pk, rsk, rpk = env
+    rng = np.random.default_rng(19)
+    H = rng.normal(size=(3, 1536)) * 0.1
+    proj = _projections(rng, 3, 1536, ranks=[16, 16, 7], d_outs=[64, 32, 5])
+    whole = zero_moai.LoraSet(eng, 3, proj)
+    eng._split_rescale_decrypt(True)
+    try:
+        split = zero_moai.LoraSet(eng, 3, proj)
+    finally:
+        eng._split_rescale_decrypt(False)
+    seeds = [61, 62, 63]
+    gw, sw = whole.deltas(pk, sk, H, seeds, with_intermediates=True)
+    gs, ss = split.deltas(pk, sk, H, seeds, with_intermediates=True)
+    assert np.array_equal(sw, ss)
+    assert all(np.array_equal(a, b) for a, b in zip(gw, gs))
+    packs = [(i, zero_moai.pack_rows(A, 8192)) for i, A, _ in proj]
+    pts = [eng.encode_to_ntt(p) for _, ps in packs for p in ps]
+    pin = [i for i, ps in packs for _ in ps]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=True), ss)
+    # without a rescale the option changes nothing
+    assert np.array_equal(whole.deltas(pk, sk, H, seeds, rescale=False, with_intermediates=True)[1],
+                          split.deltas(pk, sk, H, seeds, rescale=False, with_intermediates=True)[1])
+
+
+@pytest.mark.parametrize("n, moduli", [
+    (8192, None),
+    (32768, None),
+    (16384, [1099507695617, 1099506515969, 1152921504598720513]),
+])
+def test_lora_set_split_rescale_decrypt_matches_oracle(n, moduli):
+    """The split-kernel rescale-decrypt at log N = 13 and 15 (default chains) and on a 40-bit
+    limb 0 (FP64 transforms, last-limb values reduced by Barrett) against the oracle."""
+    eng = tensafe_he.CkksContext(n, moduli=moduli)
+    ref = orc.Context(n, moduli=moduli) if moduli else orc.Context(n)
+    sk, rsk = eng.keygen(seed=7), ref.keygen(7)
+    pk, rpk = eng.keygen_public(sk, seed=8), ref.keygen_public(rsk, 8)
+    rng = np.random.default_rng(n % 1000 + 3)
+    d = {8192: 512, 16384: 1536, 32768: 2048}[n]  # cols = 8, 5, 8
+    H = rng.normal(size=(2, d)) * 0.1
+    proj = _projections(rng, 2, d, ranks=[9, 4], d_outs=[12, 6])
+    eng._split_rescale_decrypt(True)
+    ls = zero_moai.LoraSet(eng, 2, proj)
+    seeds = [71, 72]
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, True)
+    _check(got, got_sums, exp, exp_sums)
 
 
 def test_lora_set_serial_sampler_path(env):
