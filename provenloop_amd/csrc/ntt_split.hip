@@ -818,24 +818,26 @@ __global__ __launch_bounds__(64) void rd_column_sums_kernel(RescaleDecryptArgs a
   }
 }
 
-// Step 5. One wavefront per batch: for each segment, the sum over groups of
-// 64 consecutive lanes t by a butterfly tree, the groups added in order.
+// Step 5. One wavefront per batch and segment: the sum over groups of 64
+// consecutive lanes t by a butterfly tree, the groups added in order (every
+// group's values requested first, the trees independent of one another).
 template <int LOGN>
 __global__ __launch_bounds__(64) void rd_sums_final_kernel(RescaleDecryptArgs a, const double* __restrict__ partials) {
-  constexpr uint32_t T = 1u << (LOGN - 4);
-  const uint32_t b = blockIdx.x, lane = threadIdx.x;
+  constexpr uint32_t T = 1u << (LOGN - 4), G = T / 64;
+  const uint32_t b = blockIdx.x / a.cols, c = blockIdx.x % a.cols, lane = threadIdx.x;
   const RescaleDecryptJob jb = a.jobs[b];
-  const GPtr<double> in = gld(partials) + (size_t)b * a.cols * T;
-  for (uint32_t c = 0; c < a.cols; ++c) {
-    double t = 0.0;
-    for (uint32_t w = 0; w < T / 64; ++w) {
-      double v = in[(size_t)c * T + w * 64 + lane];
+  const GPtr<double> in = gld(partials) + ((size_t)b * a.cols + c) * T + lane;
+  double v[G];
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-      t += v;
-    }
-    if (lane == 0) gst(jb.seg)[c] = t / jb.scale;
-  }
+  for (uint32_t w = 0; w < G; ++w) v[w] = in[w * 64];
+#pragma unroll
+  for (uint32_t w = 0; w < G; ++w)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v[w] += __shfl_xor(v[w], off);
+  double t = 0.0;
+#pragma unroll
+  for (uint32_t w = 0; w < G; ++w) t += v[w];
+  if (lane == 0) gst(jb.seg)[c] = t / jb.scale;
 }
 
 template <int LOGN>
@@ -848,7 +850,7 @@ static hipError_t launch_rd_split_t(const NttArgs& inv, const RescaleDecryptArgs
   hipLaunchKernelGGL((rd_column_kernel<LOGN>), dim3(2 * nb * S::PARTS), block, 0, s, inv, a.rc, a.lc);
   hipLaunchKernelGGL((rd_row_kernel<LOGN>), dim3(nb * S::PARTS), block, 0, s, a);
   hipLaunchKernelGGL((rd_column_sums_kernel<LOGN>), dim3(nb * S::PARTS), block, 0, s, a, partials);
-  hipLaunchKernelGGL((rd_sums_final_kernel<LOGN>), dim3(nb), block, 0, s, a, (const double*)partials);
+  hipLaunchKernelGGL((rd_sums_final_kernel<LOGN>), dim3(nb * a.cols), block, 0, s, a, (const double*)partials);
   return hipGetLastError();
 }
 
