@@ -99,11 +99,20 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
  *   which queues a flagged token again (and, in order, the tokens queued after
  *   it) before returning. A wider band only makes the host redraw more often
  *   (tests use it to exercise that path).
- * TH_OPT_SPLIT_RESCALE_DECRYPT: 1 makes LoRA sets created afterwards rescale
- *   and decrypt their products on the split kernels also where one
- *   workgroup per product would serve (N <= 16384, at most 256 batches);
- *   the results are the same bit for bit; testing and measurement only. */
-enum { TH_OPT_SAMPLER = 1, TH_OPT_FORCE_SERIAL_SAMPLER = 2, TH_OPT_SAMPLER_BAND = 3, TH_OPT_SPLIT_RESCALE_DECRYPT = 4 };
+ * TH_OPT_RESCALE_DECRYPT: which kernels LoRA sets created afterwards use to
+ *   rescale and decrypt their products: TH_RD_AUTO (default) - one workgroup
+ *   per product from 160 to 256 batches at N <= 16384 (and at every batch
+ *   count below N = 8192), the split kernels otherwise; TH_RD_SPLIT - the
+ *   split kernels wherever they exist (N >= 8192); TH_RD_WHOLE - one
+ *   workgroup per product wherever it serves. The results are the same bit
+ *   for bit; testing and measurement only. */
+enum {
+  TH_OPT_SAMPLER = 1,
+  TH_OPT_FORCE_SERIAL_SAMPLER = 2,
+  TH_OPT_SAMPLER_BAND = 3,
+  TH_OPT_RESCALE_DECRYPT = 4
+};
+enum { TH_RD_AUTO = 0, TH_RD_SPLIT = 1, TH_RD_WHOLE = 2 };
 enum { TH_SAMPLER_DEVICE = 0, TH_SAMPLER_HOST = 1 };
 int th_ctx_set_option(th_ctx* ctx, int option, int64_t value);
 /* Counters of the context (no counterpart in the reference): the number of

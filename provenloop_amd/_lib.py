@@ -18,7 +18,8 @@ LIB_PATH = os.path.join(HERE, "libtensafe_he_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "tensafe_he.h")
 
 TH_OK, TH_EINVAL, TH_EDEVICE, TH_ENOMEM, TH_ESTATE = 0, -1, -2, -3, -4
-TH_OPT_SAMPLER, TH_OPT_FORCE_SERIAL_SAMPLER, TH_OPT_SAMPLER_BAND, TH_OPT_SPLIT_RESCALE_DECRYPT = 1, 2, 3, 4
+TH_OPT_SAMPLER, TH_OPT_FORCE_SERIAL_SAMPLER, TH_OPT_SAMPLER_BAND, TH_OPT_RESCALE_DECRYPT = 1, 2, 3, 4
+TH_RD_AUTO, TH_RD_SPLIT, TH_RD_WHOLE = 0, 1, 2
 TH_SAMPLER_DEVICE, TH_SAMPLER_HOST = 0, 1
 
 VP = C.c_void_p

@@ -211,7 +211,7 @@ struct th_ctx {
   int host_sampler = 0;   // TH_OPT_SAMPLER
   int force_serial = 0;   // TH_OPT_FORCE_SERIAL_SAMPLER
   double band = SAMPLER_BAND_DEFAULT;  // TH_OPT_SAMPLER_BAND
-  int split_rd = 0;       // TH_OPT_SPLIT_RESCALE_DECRYPT
+  int rd_kernels = TH_RD_AUTO;  // TH_OPT_RESCALE_DECRYPT
   // Band flags of the device sampler (BandArgs): pinned host bytes the
   // kernels write through bflag_dev. A call takes a region of one byte per
   // sampled input (take_flags); asynchronous tokens keep theirs until the
@@ -932,6 +932,10 @@ const double* seg_pairs(th_ctx* c, uint32_t d) {
 // Scratch lives in the caller's scope.
 // The decrypt transform can produce segment sums itself (NTT_STORE_SEGSUM)
 // when its batch runs in the whole-polynomial kernel.
+// Fewest batches for which a LoRA set rescales and decrypts with one
+// workgroup per product by default (build_lora).
+constexpr uint32_t RD_WHOLE_MIN_BATCHES = 160;
+
 bool segsum_in_transform(const th_ctx* c, uint32_t jobs, uint32_t cols) {
   return c->logn <= 14 && jobs <= 256 && cols >= 1 && cols <= NTT_SEGSUM_FUSED_MAX_COLS;
 }
@@ -1507,8 +1511,9 @@ int th_ctx_set_option(th_ctx* ctx, int option, int64_t value) {
         need(value >= -52 && value <= -1, "sampler band must be 2^v for v in [-52, -1]");
         ctx->band = std::ldexp(1.0, (int)value);
         break;
-      case TH_OPT_SPLIT_RESCALE_DECRYPT:
-        ctx->split_rd = value != 0;
+      case TH_OPT_RESCALE_DECRYPT:
+        need(value == TH_RD_AUTO || value == TH_RD_SPLIT || value == TH_RD_WHOLE, "unknown rescale-decrypt kernels");
+        ctx->rd_kernels = (int)value;
         break;
       default:
         raise(TH_EINVAL, "unknown option " + std::to_string(option));
@@ -1984,12 +1989,20 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   const uint32_t nl_n = (scale_n > 1.5 * kScale && L >= 2) ? 2 : 1;
   const uint32_t nl_r = (scale_r > 1.5 * kScale && Lr >= 2) ? 2 : 1;
   // rescaled products straight into segment sums where the decryption reads
-  // limb 0: one workgroup per product (rescale_decrypt_kernel) where its
-  // transform can sum the segments, else the split kernels
-  // (launch_rescale_decrypt_split)
+  // limb 0: one workgroup per product (rescale_decrypt_kernel) or the split
+  // kernels (launch_rescale_decrypt_split). The first serves one round of
+  // workgroups (at most 256 batches, N <= 16384); it takes two transforms'
+  // time whatever the batch count, while the split kernels' time grows with
+  // it: at N = 16384 a token measured 0.153 against 0.097 ms with 8 batches,
+  // 0.180 against 0.176 with 128, 0.216 against 0.220 with 192 and 0.230
+  // against 0.241 with 224 (one workgroup per product first).
   const bool rd_ok = L >= 2 && nl_r == 1 && cols >= 1 && cols <= NTT_SEGSUM_FUSED_MAX_COLS;
-  const bool rd_whole = rd_ok && !c->split_rd && segsum_in_transform(c, nb, cols);
-  const bool rd_split = rd_ok && !rd_whole && c->logn >= 13;
+  const bool split_ok = c->logn >= 13;
+  const bool whole_ok = segsum_in_transform(c, nb, cols);
+  bool rd_whole = rd_ok && whole_ok;
+  if (split_ok && c->rd_kernels == TH_RD_SPLIT) rd_whole = false;
+  if (split_ok && c->rd_kernels == TH_RD_AUTO && nb < RD_WHOLE_MIN_BATCHES) rd_whole = false;
+  const bool rd_split = rd_ok && !rd_whole && split_ok;
   const bool fused_rd = rd_whole || rd_split;
   set->rd_split = rd_split;
   if (rd_split) set->rd_partials = (double*)set->alloc((size_t)nb * cols * (N / 16) * 8);

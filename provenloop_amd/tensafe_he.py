@@ -465,10 +465,12 @@ class CkksContext:
         _lib.check(_lib.load().th_ctx_stats(self._h, C.byref(v)))
         return v.value
 
-    def _split_rescale_decrypt(self, on: bool):
-        """Testing hook: LoRA sets created afterwards rescale and decrypt on the
-        split kernels also where one workgroup per product would serve."""
-        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_SPLIT_RESCALE_DECRYPT, int(on)))
+    def _rescale_decrypt_kernels(self, which: str):
+        """Testing hook: the kernels LoRA sets created afterwards rescale and
+        decrypt with: "auto" (default), "split" or "whole" (one workgroup per
+        product wherever it serves); the results are the same bit for bit."""
+        value = {"auto": _lib.TH_RD_AUTO, "split": _lib.TH_RD_SPLIT, "whole": _lib.TH_RD_WHOLE}[which]
+        _lib.check(_lib.load().th_ctx_set_option(self._h, _lib.TH_OPT_RESCALE_DECRYPT, value))
 
     def _force_serial_sampler(self, on: bool):
         """Testing hook: replay every device stream serially (the rejection path)."""

@@ -291,7 +291,7 @@ def test_lora_set_rescale_decrypt_chains(n, moduli, d):
     rng = np.random.default_rng(n + moduli[0] % 1000)
     H = rng.normal(size=(2, d)) * 0.1
     proj = _projections(rng, 2, d, ranks=[16, 7], d_outs=[24, 9])
-    ls = zero_moai.LoraSet(eng, 2, proj)
+    ls = _set_with(eng, "whole", 2, proj)
     seeds = [31, 32]
     got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=True, with_intermediates=True)
     packs = [(i, zero_moai.pack_rows(A, n // 2)) for i, A, _ in proj]
@@ -330,20 +330,24 @@ def test_lora_set_many_batches_rescale(env):
     _check(got[:2], got_sums[:8], exp, exp_sums)
 
 
+def _set_with(eng, kernels, n_inputs, proj):
+    eng._rescale_decrypt_kernels(kernels)
+    try:
+        return zero_moai.LoraSet(eng, n_inputs, proj)
+    finally:
+        eng._rescale_decrypt_kernels("auto")
+
+
 def test_lora_set_split_rescale_decrypt_equals_whole(env):
-    """The split-kernel rescale-decrypt (forced where one workgroup per product would serve)
-    gives the same segment sums and deltas, bit for bit, as the one-workgroup kernel and as
-    th_lora_a_pass, at the full token shape's 4 batches per projection."""
+    """The split-kernel rescale-decrypt and the one-workgroup kernel (each forced) give the same
+    segment sums and deltas, bit for bit, and the same as th_lora_a_pass, at the full token
+    shape's 4 batches per projection."""
     eng, ref, sk, pk, rsk, rpk = env
     rng = np.random.default_rng(19)
     H = rng.normal(size=(3, 1536)) * 0.1
     proj = _projections(rng, 3, 1536, ranks=[16, 16, 7], d_outs=[64, 32, 5])
-    whole = zero_moai.LoraSet(eng, 3, proj)
-    eng._split_rescale_decrypt(True)
-    try:
-        split = zero_moai.LoraSet(eng, 3, proj)
-    finally:
-        eng._split_rescale_decrypt(False)
+    whole = _set_with(eng, "whole", 3, proj)
+    split = _set_with(eng, "split", 3, proj)
     seeds = [61, 62, 63]
     gw, sw = whole.deltas(pk, sk, H, seeds, with_intermediates=True)
     gs, ss = split.deltas(pk, sk, H, seeds, with_intermediates=True)
@@ -374,8 +378,7 @@ def test_lora_set_split_rescale_decrypt_matches_oracle(n, moduli):
     d = {8192: 512, 16384: 1536, 32768: 2048}[n]  # cols = 8, 5, 8
     H = rng.normal(size=(2, d)) * 0.1
     proj = _projections(rng, 2, d, ranks=[9, 4], d_outs=[12, 6])
-    eng._split_rescale_decrypt(True)
-    ls = zero_moai.LoraSet(eng, 2, proj)
+    ls = _set_with(eng, "split", 2, proj)
     seeds = [71, 72]
     got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
     exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, True)
