@@ -14,11 +14,15 @@
 // a CU cannot overlap one polynomial's loads with another's arithmetic; the
 // split kernels move the data twice but keep many wavefronts per CU. The
 // whole-polynomial kernel's time grows in steps of one round of workgroups
-// (one per CU); measured on MI355X at N = 16384 it wins for one round (256
-// transforms: 40 us vs 46 us forward) and the split kernels win from 384
-// transforms on (1792: 197 us vs 256 us). So batches of at most
-// NTT_WHOLE_MAX_JOBS = 256 (the CU count) use the first, larger ones the
-// second.
+// (one per CU) and a round takes a transform's time however few workgroups
+// it holds, while the split kernels spread every transform over 16
+// workgroups. Measured on MI355X at N = 16384 (forward, 4-limb chain): 4
+// transforms 23.8 us whole against 11.0 us split, 64: 25.2 against 19.5,
+// 128: 26.5 against 32.6, 256: 29.2 against 35.9; from 384 transforms on the
+// split kernels win again (1792: 197 us against 256 us). So batches of
+// NTT_WHOLE_MIN_JOBS = 96 to NTT_WHOLE_MAX_JOBS = 256 (the CU count) use the
+// first, the others the second (the segment-sum epilogue exists in the first
+// only).
 //
 // Whole-polynomial kernel: T = N/16 threads hold 16 coefficients each in
 // registers; a register pass performs up to 4 butterfly stages on the
@@ -45,6 +49,9 @@ constexpr int NTT_SPLIT_MIN_LOGN = 13;
 constexpr int NTT_WHOLE_MAX_LOGN = 14;
 #ifndef NTT_WHOLE_MAX_JOBS
 #define NTT_WHOLE_MAX_JOBS 256
+#endif
+#ifndef NTT_WHOLE_MIN_JOBS
+#define NTT_WHOLE_MIN_JOBS 96
 #endif
 hipError_t launch_ntt_split(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s);
 hipError_t launch_rescale_split(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf,
@@ -452,8 +459,12 @@ static hipError_t launch_one(const NttArgs& a, uint32_t njobs, hipStream_t s) {
                   });
 }
 
-static bool use_split(int logn, uint32_t njobs) {
+// Sizes and batches the whole-polynomial kernel cannot serve.
+static bool whole_unavailable(int logn, uint32_t njobs) {
   return logn >= NTT_SPLIT_MIN_LOGN && (logn > NTT_WHOLE_MAX_LOGN || njobs > NTT_WHOLE_MAX_JOBS);
+}
+static bool use_split(int logn, uint32_t njobs) {
+  return whole_unavailable(logn, njobs) || (logn >= NTT_SPLIT_MIN_LOGN && njobs < NTT_WHOLE_MIN_JOBS);
 }
 
 hipError_t launch_rescale(int logn, const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nfwd,
@@ -487,11 +498,11 @@ hipError_t launch_encrypt(int logn, const NttArgs& a, uint32_t ninputs, uint32_t
 
 hipError_t launch_ntt(int logn, bool inverse, const NttArgs& a, uint32_t njobs, hipStream_t s) {
   if (njobs == 0) return hipSuccess;
-  if (a.jobs && a.store == NTT_STORE_SEGSUM &&
-      (!inverse || use_split(logn, njobs) || logn > NTT_WHOLE_MAX_LOGN || a.cols < 1 ||
-       a.cols > NTT_SEGSUM_FUSED_MAX_COLS))
+  const bool segsum = a.jobs && a.store == NTT_STORE_SEGSUM;
+  if (segsum && (!inverse || whole_unavailable(logn, njobs) || logn > NTT_WHOLE_MAX_LOGN || a.cols < 1 ||
+                 a.cols > NTT_SEGSUM_FUSED_MAX_COLS))
     return hipErrorInvalidValue;  // the segment-sum epilogue exists in the whole-polynomial inverse only
-  if (use_split(logn, njobs)) return launch_ntt_split(logn, inverse, a, njobs, s);
+  if (!segsum && use_split(logn, njobs)) return launch_ntt_split(logn, inverse, a, njobs, s);
 #define TH_NTT_CASE(L) \
   case L: return inverse ? launch_one<L, true>(a, njobs, s) : launch_one<L, false>(a, njobs, s);
   switch (logn) {
