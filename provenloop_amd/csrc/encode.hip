@@ -18,19 +18,19 @@ namespace th {
 
 constexpr int ENC_THREADS = 1024;
 
+// Part `part` of encode job `job`: the first lb = logn - LP stages of the
+// N-point transform over the elements whose bit-reversed position lies in the
+// part, in LDS (sh), written to the job's parts scratch. Any block size works:
+// every loop strides by blockDim.x.
 template <int LP>
-__global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* __restrict__ jobs,
-                                                              const double* __restrict__ stage_re,
-                                                              const double* __restrict__ stage_im, uint32_t logn,
-                                                              const double* __restrict__ z_base,
-                                                              const SampleJob* __restrict__ fix, SeedBlock sb,
-                                                              int use_sb, int force_serial, BandArgs band) {
-  extern __shared__ double sh[];
+__device__ __forceinline__ void encode_part(const EncodeJob* __restrict__ jobs, const double* __restrict__ stage_re,
+                                            const double* __restrict__ stage_im, uint32_t logn,
+                                            const double* __restrict__ z_base, uint32_t part, uint32_t job,
+                                            double* sh) {
   const uint32_t n = 1u << logn, S = n / 2;
   const uint32_t M = n >> LP;
-  const uint32_t part = blockIdx.x;
-  const EncodeJob jb = jobs[blockIdx.y];
-  const GPtr<double> z = gld(z_base ? z_base + (size_t)blockIdx.y * (jb.rep_d ? jb.rep_d : S) : jb.z);
+  const EncodeJob jb = jobs[job];
+  const GPtr<double> z = gld(z_base ? z_base + (size_t)job * (jb.rep_d ? jb.rep_d : S) : jb.z);
   const uint32_t MP = fft_pad(M);  // padded length of re and im
   double* re = sh;
   double* im = sh + MP;
@@ -121,12 +121,41 @@ __global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* _
       }
     }
   }
-  // the sampler launch queued before this one left its rejection check here
-  if (fix && part == 0 && threadIdx.x == 0) {
-    const SampleJob sj = fix[blockIdx.y];
-    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial,
-                   band.flags ? band.flags + blockIdx.y : nullptr, band.band);
+}
+
+template <int LP>
+__global__ __launch_bounds__(ENC_THREADS) void k_encode_parts(const EncodeJob* __restrict__ jobs,
+                                                              const double* __restrict__ stage_re,
+                                                              const double* __restrict__ stage_im, uint32_t logn,
+                                                              const double* __restrict__ z_base) {
+  extern __shared__ double sh[];
+  encode_part<LP>(jobs, stage_re, stage_im, logn, z_base, blockIdx.x, blockIdx.y, sh);
+}
+
+// k_encode_parts with the sampler's blocks of the same jobs (sample[y] for
+// encode job y) as further workgroups: x < 2^LP encodes part x, every later
+// workgroup draws SPT * SAMPLE_ENC_THREADS ChaCha20 blocks of job y's stream,
+// one per thread per step (k_sample_blocks' work). The sampler's VALU-bound
+// workgroups and the encoder's latency-bound ones share the CUs instead of
+// running one launch after the other.
+constexpr uint32_t SAMPLE_ENC_THREADS = 256;
+template <int LP, int SPT>
+__global__ __launch_bounds__(SAMPLE_ENC_THREADS) void k_sample_encode_parts(
+    const EncodeJob* __restrict__ jobs, const double* __restrict__ stage_re, const double* __restrict__ stage_im,
+    uint32_t logn, const double* __restrict__ z_base, const SampleJob* __restrict__ sample, SeedBlock sb, int use_sb,
+    BandArgs band) {
+  extern __shared__ double sh[];
+  constexpr uint32_t P = 1u << LP;
+  if (blockIdx.x < P) {
+    encode_part<LP>(jobs, stage_re, stage_im, logn, z_base, blockIdx.x, blockIdx.y, sh);
+    return;
   }
+  const SampleJob jb = sample[blockIdx.y];
+  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.y);
+  uint8_t* flag = band.flags ? band.flags + blockIdx.y : nullptr;
+  const uint32_t b0 = (blockIdx.x - P) * SPT * SAMPLE_ENC_THREADS + threadIdx.x;
+#pragma unroll 1
+  for (int k = 0; k < SPT; ++k) sample_block(jb, seed, 1u << logn, b0 + k * SAMPLE_ENC_THREADS, band.band, flag);
 }
 
 // Rust `f64::round() as i64`: half away from zero, saturating, NaN -> 0.
@@ -202,10 +231,19 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
                                                       const double* __restrict__ twist_im,
                                                       const double* __restrict__ stage_re,
                                                       const double* __restrict__ stage_im, uint32_t logn,
-                                                      uint32_t L) {
+                                                      uint32_t L, const SampleJob* __restrict__ fix, SeedBlock sb,
+                                                      int use_sb, int force_serial, BandArgs band) {
   constexpr int P = 1 << LP;
   constexpr int G = P >= 4 ? P / 4 : 1;
   const uint32_t n = 1u << logn, lb = logn - LP;
+  // the sampler's blocks of this launch's jobs ran before this kernel: replay
+  // a job whose u words held a rejected value (jobs with fix write mvals, so
+  // no thread of this kernel reads the randomness being rewritten)
+  if (fix && blockIdx.x == 0 && threadIdx.x == 0) {
+    const SampleJob sj = fix[blockIdx.y];
+    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial,
+                   band.flags ? band.flags + blockIdx.y : nullptr, band.band);
+  }
   const uint32_t M = n >> LP;
   const EncodeJob jb = jobs[blockIdx.y];
   const GPtr<double> Pd = gld(jb.parts);
@@ -294,16 +332,18 @@ size_t encode_parts_doubles(uint32_t logn) { return (size_t)2 << logn; }
 
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s, const double* z_base, const SampleJob* fix, const uint64_t* seeds,
-                         int force_serial, BandArgs band, uint32_t fold, uint32_t fold_limbs) {
+                         uint32_t L, hipStream_t s, const double* z_base, const SampleJob* sample,
+                         const uint64_t* seeds, int force_serial, BandArgs band, uint32_t fold, uint32_t fold_limbs) {
   if (!njobs) return hipSuccess;
-  if (fix && njobs > SEEDS_PER_LAUNCH) return hipErrorInvalidValue;
+  const uint32_t n = 1u << logn;
+  if (sample && (njobs > SEEDS_PER_LAUNCH || fold || n % 16)) return hipErrorInvalidValue;
   if (fold && (njobs % fold || !fold_limbs || __builtin_popcount(fold_limbs) > (int)ENC_FOLD_MAX_LIMBS ||
                (L < 32 && fold_limbs >> L)))
     return hipErrorInvalidValue;
   SeedBlock sb{};
-  if (fix && seeds)
+  if (sample && seeds)
     for (uint32_t i = 0; i < njobs; ++i) sb.v[i] = seeds[i];
+  const int use_sb = seeds != nullptr;
   // parts of at most 4096 values (two workgroups' LDS per CU; with 672
   // encodes of N=16384 per CryptoMOE token, the token measured 0.656 ms with
   // 4096-value parts against 0.697 ms with 8192, 0.675 ms with 2048 and
@@ -313,26 +353,58 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
   const uint32_t lp_min = fft_parts_log(logn);
   uint32_t lp = logn > 12 && logn - 12 > lp_min ? logn - 12 : lp_min;
   while (lp < 4 && logn - lp > 10 && njobs * (1u << lp) < 512) ++lp;
-  const uint32_t M = (1u << logn) >> lp;
+  const uint32_t M = n >> lp;
   // padded values (+ twiddles with 8 or more parts)
   const size_t lds = ((size_t)2 * fft_pad(M) + (lp >= 3 ? (size_t)2 * M : 0)) * sizeof(double);
   // dit_stages_reg needs 8 values per thread at most
   const uint32_t threads = M / 8 < 64 ? 64 : (M / 8 > ENC_THREADS ? ENC_THREADS : M / 8);
   const uint32_t fin = lp >= 2 ? M << (lp - 2) : M;  // threads of the final kernel per encode
   const uint32_t gx = (fin + 255) / 256 < 32 ? (fin + 255) / 256 : 32;
+  // With sample, the sampler's workgroups join the parts kernel while a part
+  // leaves LDS for several workgroups per CU (at most 1024 values, 34 KiB:
+  // four per CU); each thread draws two blocks where one each would make more
+  // workgroups than the CUs hold at once. Per token of 28 encodes at
+  // N=16384: 0.2241 ms with two blocks per thread, 0.2249 ms with one,
+  // 0.2296 ms with the sampler launched on its own before the encoder.
+  // Larger parts keep a sampler launch of their own. Either way the final
+  // kernel finishes the rejection handling.
+  const bool merge = sample && M <= 1024;
   hipError_t e;
-#define TH_ENC(LP)                                                                                         \
-  case LP:                                                                                                 \
-    e = allow_full_lds<k_encode_parts<LP>>();                                                              \
-    if (e != hipSuccess) return e;                                                                         \
-    hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,   \
-                       stage_im, logn, z_base, fix, sb, (int)(seeds != nullptr), force_serial, band);     \
-    if (fold)                                                                                              \
-      hipLaunchKernelGGL(k_encode_final_fold<LP>, dim3(gx, njobs / fold), dim3(256), 0, s, jobs, fold,     \
-                         fold_limbs, bc, twist_re, twist_im, stage_re, stage_im, logn);                    \
-    else                                                                                                   \
-      hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re,         \
-                         twist_im, stage_re, stage_im, logn, L);                                           \
+  if (sample && !merge) {
+    e = launch_sample_pk(sample, njobs, n, force_serial, s, seeds, true, true, band);
+    if (e != hipSuccess) return e;
+  }
+  const uint32_t sblocks = 9 * (n / 16);  // ChaCha20 blocks per job
+  uint32_t spt = 1;
+  if (merge) {
+    constexpr uint32_t CUS = 256, WG_PER_CU_WAVES = 7;  // MI355X CUs; 28 waves per CU at this kernel's VGPRs
+    const uint32_t per_cu = (uint32_t)((160u * 1024) / lds) < WG_PER_CU_WAVES ? (uint32_t)((160u * 1024) / lds)
+                                                                              : WG_PER_CU_WAVES;
+    if (njobs * ((1u << lp) + (sblocks + SAMPLE_ENC_THREADS - 1) / SAMPLE_ENC_THREADS) > CUS * per_cu) spt = 2;
+  }
+  const uint32_t sx = (sblocks + spt * SAMPLE_ENC_THREADS - 1) / (spt * SAMPLE_ENC_THREADS);
+#define TH_ENC(LP)                                                                                              \
+  case LP:                                                                                                      \
+    if (merge) {                                                                                                \
+      const dim3 grid((1u << LP) + sx, njobs);                                                                  \
+      if (spt == 2)                                                                                             \
+        hipLaunchKernelGGL((k_sample_encode_parts<LP, 2>), grid, dim3(SAMPLE_ENC_THREADS), lds, s, jobs,        \
+                           stage_re, stage_im, logn, z_base, sample, sb, use_sb, band);                         \
+      else                                                                                                      \
+        hipLaunchKernelGGL((k_sample_encode_parts<LP, 1>), grid, dim3(SAMPLE_ENC_THREADS), lds, s, jobs,        \
+                           stage_re, stage_im, logn, z_base, sample, sb, use_sb, band);                         \
+    } else {                                                                                                    \
+      e = allow_full_lds<k_encode_parts<LP>>();                                                                 \
+      if (e != hipSuccess) return e;                                                                            \
+      hipLaunchKernelGGL(k_encode_parts<LP>, dim3(1u << LP, njobs), dim3(threads), lds, s, jobs, stage_re,      \
+                         stage_im, logn, z_base);                                                               \
+    }                                                                                                           \
+    if (fold)                                                                                                   \
+      hipLaunchKernelGGL(k_encode_final_fold<LP>, dim3(gx, njobs / fold), dim3(256), 0, s, jobs, fold,          \
+                         fold_limbs, bc, twist_re, twist_im, stage_re, stage_im, logn);                         \
+    else                                                                                                        \
+      hipLaunchKernelGGL(k_encode_final<LP>, dim3(gx, njobs), dim3(256), 0, s, jobs, bc, twist_re, twist_im,    \
+                         stage_re, stage_im, logn, L, sample, sb, use_sb, force_serial, band);                  \
     return hipGetLastError();
   switch (lp) {
     TH_ENC(0)

@@ -39,10 +39,11 @@ constexpr double SAMPLER_BAND_DEFAULT = 0x1p-36;
 
 // Encode z and write the per-limb residues of m (+ e0), e1 and u. With
 // z_base, job i reads its input at z_base + i * (rep_d, or N/2 without
-// replication) instead of its z field. With fix (the sample jobs of a
-// flagged launch_sample_pk queued just before with fix_later, one per encode
-// job, at most SEEDS_PER_LAUNCH of them, and the same seeds), the launch also
-// finishes the sampler's rejection handling (k_sample_fix's work). With fold
+// replication) instead of its z field. With sample (one flagged sampler job
+// per encode job, at most SEEDS_PER_LAUNCH of them, seeds as in
+// launch_sample_pk; the encode jobs must write mvals), the launch also draws
+// those jobs' encrypt_pk randomness, as launch_sample_pk(flagged) would,
+// rejection handling and band flags included. With fold
 // > 0, every fold consecutive jobs are summed into one residue polynomial
 // (the experts of a mixture batch): the group's first job's dst receives, on
 // the limbs in fold_limbs (at most ENC_FOLD_MAX_LIMBS), the sum mod q_l of
@@ -50,7 +51,7 @@ constexpr double SAMPLER_BAND_DEFAULT = 0x1p-36;
 constexpr uint32_t ENC_FOLD_MAX_LIMBS = 4;
 hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettConst* bc, const double* twist_re,
                          const double* twist_im, const double* stage_re, const double* stage_im, uint32_t logn,
-                         uint32_t L, hipStream_t s, const double* z_base = nullptr, const SampleJob* fix = nullptr,
+                         uint32_t L, hipStream_t s, const double* z_base = nullptr, const SampleJob* sample = nullptr,
                          const uint64_t* seeds = nullptr, int force_serial = 0, BandArgs band = BandArgs{nullptr, 0.0},
                          uint32_t fold = 0, uint32_t fold_limbs = 0);
 size_t encode_parts_doubles(uint32_t logn);

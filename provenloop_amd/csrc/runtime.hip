@@ -2225,18 +2225,18 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
                  const uint64_t* seeds, int do_rescale, double* dout, bool host_draw, BandArgs band) {
   const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
   hipStream_t st = ctx->stream;
-  // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the sampler launch
-  // the encoder launch (next on the stream) finishes the sampler's rejection
-  // check when every input's seed fits one launch
-  const bool fix_in_encode = !host_draw && ni <= SEEDS_PER_LAUNCH;
+  // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the
+  // launch. When every input's seed fits one launch, the encoder's launch
+  // draws the randomness too (the sampler's workgroups beside the encoder's)
+  const bool sample_in_encode = !host_draw && ni <= SEEDS_PER_LAUNCH;
   if (host_draw) {
     OpScope sc(ctx);
     upload_host_draws(sc, seeds, ni, set->u, set->e0, set->e1);
-  } else {
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, fix_in_encode, band));
+  } else if (!sample_in_encode) {
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, false, band));
   }
   HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                       ctx->d_stage_im, ctx->logn, L, st, z, fix_in_encode ? set->d_sample : nullptr, seeds,
+                       ctx->d_stage_im, ctx->logn, L, st, z, sample_in_encode ? set->d_sample : nullptr, seeds,
                        ctx->force_serial, band));
   // D = c0 + c1 s, all the decryption reads of an input's limbs 0..nl-1
   // (k_key_dot, or formed by the encrypt row passes in place of those limbs

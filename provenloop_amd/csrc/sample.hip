@@ -27,36 +27,8 @@ namespace th {
 __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, SeedBlock sb, int use_sb,
                                 BandArgs band) {
   const SampleJob jb = jobs[blockIdx.y];
-  const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.y);
-  const uint32_t nblocks = 9 * (n / 16);
-  const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nblocks) return;
-  uint32_t w[16];
-  chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
-  if (b < n / 16) {
-    bool zero = false;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      gst(jb.u)[16 * b + i] = ternary_value(w[i]);
-      zero |= w[i] == 0;
-    }
-    if (zero && jb.reject) atomicOr(jb.reject, 1u);  // range_u32 rejects 0 (rng.rs:112-119)
-  } else {
-    const uint32_t g0 = (16 * b - n) / 4;
-    bool any = false;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t g = g0 + t;
-      bool near;
-      const int64_t e = gaussian_rounded(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3], band.band, near);
-      any |= near;
-      if (g < n)
-        gst(jb.e0)[g] = e;
-      else
-        gst(jb.e1)[g - n] = e;
-    }
-    if (any && band.flags) band.flags[blockIdx.y] = 1;  // a plain store; rare
-  }
+  sample_block(jb, job_seed(jb, sb, use_sb, blockIdx.y), n, blockIdx.x * blockDim.x + threadIdx.x, band.band,
+               band.flags ? band.flags + blockIdx.y : nullptr);
 }
 
 // One workgroup per job: re-derive the u words; if any was rejected (== 0),

@@ -1,6 +1,7 @@
 // Device side of the encrypt_pk sampler (tensafe-he-core/src/rng.rs:31-157,
 // sampling.rs:17-64, ciphertext.rs:255-273), shared by the sampler kernels
-// and by the encoder launch that finishes the sampler's rejection handling.
+// and by the encoder's kernels, which can draw a token's randomness beside the
+// encoding and finish the sampler's rejection handling.
 #pragma once
 #include "encode_sample.h"
 
@@ -63,6 +64,41 @@ static __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t
   if (r >= 9223372036854775808.0) return INT64_MAX;
   if (r < -9223372036854775808.0) return INT64_MIN;
   return (int64_t)r;
+}
+
+// Block b (one ChaCha20 block of 16 words) of job jb's stream: the u values
+// of words [16 b, 16 b + 16) while they lie below n, else four Gaussian draws
+// (g = (16 b - n) / 4 onwards, e0 then e1). A zero u word sets the job's
+// reject flag; a draw within `band` of a rounding boundary sets *flag.
+static __device__ __forceinline__ void sample_block(const SampleJob& jb, uint64_t seed, uint32_t n, uint32_t b,
+                                                    double band, uint8_t* flag) {
+  if (b >= 9 * (n / 16)) return;
+  uint32_t w[16];
+  chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
+  if (b < n / 16) {
+    bool zero = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      gst(jb.u)[16 * b + i] = ternary_value(w[i]);
+      zero |= w[i] == 0;
+    }
+    if (zero && jb.reject) atomicOr(jb.reject, 1u);  // range_u32 rejects 0 (rng.rs:112-119)
+  } else {
+    const uint32_t g0 = (16 * b - n) / 4;
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t g = g0 + t;
+      bool near;
+      const int64_t e = gaussian_rounded(w[4 * t], w[4 * t + 1], w[4 * t + 2], w[4 * t + 3], band, near);
+      any |= near;
+      if (g < n)
+        gst(jb.e0)[g] = e;
+      else
+        gst(jb.e1)[g - n] = e;
+    }
+    if (any && flag) *flag = 1;  // a plain store; rare
+  }
 }
 
 // Seeds of up to SEEDS_PER_LAUNCH jobs passed with the launch itself, so a
