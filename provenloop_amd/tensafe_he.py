@@ -444,7 +444,9 @@ class CkksContext:
         return x
 
     def sync(self):
-        _lib.check(_lib.load().th_ctx_sync(self._h))
+        rc = _lib.load().th_ctx_sync(self._h)
+        if rc:
+            _lib.check(rc)
 
     def set_sampler(self, where: str):
         """Where seeded encrypt_pk draws its randomness: "device" (default) or "host"."""

@@ -244,6 +244,9 @@ class LoraSet:
         sd = np.ascontiguousarray(seeds, np.uint64)
         if sd.shape != (self.n_inputs,):
             raise ValueError("need one seed per input")
-        _lib.check(self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk),
-                                            C.c_void_p(hidden_dev), 1, _lib.ptr(sd), int(bool(rescale)),
-                                            C.c_void_p(dev_out), 1, None))
+        # plain ints for the pointer arguments (the binding declares them
+        # c_void_p): this call is on the per-token path
+        rc = self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk), hidden_dev, 1,
+                                      sd.ctypes.data, 1 if rescale else 0, dev_out, 1, None)
+        if rc:
+            _lib.check(rc)

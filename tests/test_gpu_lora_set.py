@@ -257,6 +257,30 @@ def test_lora_set_split_sizes_n8192():
         _check(got[i:i + 1], got_sums[i:i + 1], exp, exp_sums)
 
 
+@pytest.mark.parametrize("n_in", [64, 65])
+def test_lora_set_sampler_in_encoder_launch_limit(n_in):
+    """Up to 64 inputs (one launch's seeds) the encoder's first launch also draws the
+    randomness (the sampler's workgroups beside the encoder's, two blocks per thread at
+    this size); 65 take the sampler's own launches. Either way every input's segment sums
+    equal th_lora_a_pass's (its own sampler launch) bit for bit, and the first and last
+    inputs match the oracle."""
+    eng, ref = tensafe_he.CkksContext(8192), orc.Context(8192)
+    sk, rsk = eng.keygen(seed=7), ref.keygen(7)
+    pk, rpk = eng.keygen_public(sk, seed=8), ref.keygen_public(rsk, 8)
+    rng = np.random.default_rng(90 + n_in)
+    d = 512
+    H = rng.normal(size=(n_in, d)) * 0.1
+    proj = _projections(rng, n_in, d, ranks=[4] * n_in, d_outs=[8] * n_in)
+    ls = zero_moai.LoraSet(eng, n_in, proj)
+    seeds = list(range(700, 700 + n_in))
+    got, got_sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    pts = [eng.encode_to_ntt(p) for _, A, _ in proj for p in zero_moai.pack_rows(A, 4096)]
+    assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, list(range(n_in))), got_sums)
+    for i in (0, n_in - 1):
+        exp, exp_sums = _oracle(ref, rpk, rsk, H[i:i + 1], seeds[i:i + 1], [(0, proj[i][1], proj[i][2])], True)
+        _check(got[i:i + 1], got_sums[i:i + 1], exp, exp_sums)
+
+
 def test_lora_set_crt_branch_after_rescale():
     """A chain whose last prime is 30-bit: the rescaled scale is ~2^50 > 1.5 * 2^40, so the
     decrypt takes the CRT branch over limbs 0 and 1 (ciphertext.rs:351)."""
