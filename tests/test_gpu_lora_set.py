@@ -326,6 +326,30 @@ def test_lora_set_rescale_decrypt_chains(n, moduli, d):
     _check(got, got_sums, exp, exp_sums)
 
 
+@pytest.mark.parametrize("n, d", [(1024, 128), (2048, 256)])
+def test_lora_set_small_rings(n, d):
+    """N = 1024 and 2048 on the default chain's primes (one and two encoder parts, the
+    sampler's workgroups in the same launch, whole-polynomial transforms everywhere): the
+    segment sums equal th_lora_a_pass's bit for bit and the deltas match the oracle's."""
+    q = [1152921504606748673, 1099510054913, 1099508121601, 1152921504606683137]
+    eng, ref = tensafe_he.CkksContext(n, moduli=q), orc.Context(n, moduli=q)
+    sk, rsk = eng.keygen(seed=9), ref.keygen(9)
+    pk, rpk = eng.keygen_public(sk, seed=10), ref.keygen_public(rsk, 10)
+    rng = np.random.default_rng(n)
+    H = rng.normal(size=(3, d)) * 0.1
+    proj = _projections(rng, 3, d, ranks=[8, 3, 5], d_outs=[10, 4, 7])
+    ls = zero_moai.LoraSet(eng, 3, proj)
+    seeds = [41, 42, 43]
+    for rescale in (True, False):
+        got, got_sums = ls.deltas(pk, sk, H, seeds, rescale=rescale, with_intermediates=True)
+        packs = [(i, zero_moai.pack_rows(A, n // 2)) for i, A, _ in proj]
+        pts = [eng.encode_to_ntt(p) for _, ps in packs for p in ps]
+        pin = [i for i, ps in packs for _ in ps]
+        assert np.array_equal(eng.lora_a_pass(pk, sk, H, seeds, pts, pin, rescale=rescale), got_sums)
+        exp, exp_sums = _oracle(ref, rpk, rsk, H, seeds, proj, rescale)
+        _check(got, got_sums, exp, exp_sums)
+
+
 def test_lora_set_many_batches_rescale(env):
     """260 batches, more than one round of one-workgroup-per-product kernels: the rescale and
     decryption run on the split kernels. A batch's sums depend only on its input, plaintext
