@@ -42,6 +42,7 @@ import json
 import os
 import sys
 import time
+import types
 
 import numpy as np
 
@@ -637,6 +638,27 @@ def single_delta_workload(ctx, sk, pk, cpu, reps=100, warm=10):
     }
 
 
+def run_single(args):
+    """Only the single-delta figure, for a kernel trace of its
+    launches: the same calls as the reported line's single_delta."""
+    from oracle import oracle as orc
+    from provenloop_amd import tensafe_he
+
+    ctx = tensafe_he.CkksContext(N)
+    sk = ctx.keygen(seed=11)
+    pk = ctx.keygen_public(sk, seed=22)
+    cpu = types.SimpleNamespace(ctx=orc.Context(N))
+    cpu.sk = cpu.ctx.keygen(11)
+    cpu.pk = cpu.ctx.keygen_public(cpu.sk, 22)
+    r = single_delta_workload(ctx, sk, pk, cpu, reps=args.steps, warm=args.warmup)
+    print(json.dumps(dict({
+        "metric": "latency of one encrypted LoRA delta at N=16384 (host in, host out)",
+        "n_gpus": 1, "higher_is_better": False, "dtype": "u64",
+        "data": "synthetic (seeded N(0,1)*0.1 hidden state, N(0,0.02) LoRA A)",
+        "config": {"workload": r.pop("workload"), "N": N},
+    }, **r)), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -656,15 +678,15 @@ def main():
                          "60-bit (integer butterfly path) or four 40-bit (FP64 butterfly path) primes")
     ap.add_argument("--ntt-n", type=int, choices=(16384, 32768), default=N,
                     help="ring degree of the --ntt-only launches (reference chain for that degree)")
-    ap.add_argument("--workload", choices=("token", "moe", "saturation"), default="token",
+    ap.add_argument("--workload", choices=("token", "moe", "saturation", "single"), default="token",
                     help="token: the per-token Qwen2.5-1.5B pass (the reported line); moe: its CryptoMOE "
                          "variant with a per-token gate; saturation: 32 sessions at Qwen2.5-7B shape on "
-                         "N=32768 with 8 limbs")
+                         "N=32768 with 8 limbs; single: one encrypted delta's latency")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 20 if args.workload == "saturation" else 100
     if args.warmup is None:
-        args.warmup = 3 if args.workload == "saturation" else 20
+        args.warmup = {"saturation": 3, "single": 10}.get(args.workload, 20)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by session/token "
               "with no cross-GPU exchange, so N GPUs scale the one-GPU figure)", file=sys.stderr)
@@ -677,6 +699,9 @@ def main():
         return
     if args.workload == "saturation":
         run_saturation(args)
+        return
+    if args.workload == "single":
+        run_single(args)
         return
 
     A, B = make_workload()
