@@ -377,10 +377,11 @@ hipError_t launch_encode(const EncodeJob* jobs, uint32_t njobs, const BarrettCon
   const uint32_t sblocks = 9 * (n / 16);  // ChaCha20 blocks per job
   uint32_t spt = 1;
   if (merge) {
-    constexpr uint32_t CUS = 256, WG_PER_CU_WAVES = 7;  // MI355X CUs; 28 waves per CU at this kernel's VGPRs
+    constexpr uint32_t WG_PER_CU_WAVES = 7;  // 28 waves per CU at this kernel's VGPRs
     const uint32_t per_cu = (uint32_t)((160u * 1024) / lds) < WG_PER_CU_WAVES ? (uint32_t)((160u * 1024) / lds)
                                                                               : WG_PER_CU_WAVES;
-    if (njobs * ((1u << lp) + (sblocks + SAMPLE_ENC_THREADS - 1) / SAMPLE_ENC_THREADS) > CUS * per_cu) spt = 2;
+    if (njobs * ((1u << lp) + (sblocks + SAMPLE_ENC_THREADS - 1) / SAMPLE_ENC_THREADS) > device_cu_count() * per_cu)
+      spt = 2;
   }
   const uint32_t sx = (sblocks + spt * SAMPLE_ENC_THREADS - 1) / (spt * SAMPLE_ENC_THREADS);
 #define TH_ENC(LP)                                                                                              \

@@ -2,6 +2,7 @@
 // kernel translation units. Not part of the public C ABI.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <stdint.h>
 
 #include "th_device.h"
@@ -111,6 +112,22 @@ struct RescaleDecryptArgs {
   uint32_t cols;                // segments per job, at most NTT_SEGSUM_FUSED_MAX_COLS
   uint32_t pad_;
 };
+
+// Compute units of the current device (256 on MI355X), queried once per
+// device; a launch heuristic only, so a failed query falls back to 256.
+inline uint32_t device_cu_count() {
+  static std::atomic<uint32_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  uint32_t v = cache[dev].load(std::memory_order_relaxed);
+  if (!v) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    v = (uint32_t)n;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 
 // Lets kernel K use up to the whole 160 KiB of a CU's LDS as dynamic shared
 // memory. Set once per kernel (the first call's result is kept), so launches
