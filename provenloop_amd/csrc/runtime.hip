@@ -272,7 +272,6 @@ struct th_lora {
   uint64_t* res = nullptr;     // n_batches x 2 nl_r x N: the rescaled limbs the decryption reads
   uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
   double* sums = nullptr;      // n_batches x cols
-  double* deltas = nullptr;    // n_deltas
   const SampleJob* d_sample = nullptr;
   const EncCombineJob* d_comb = nullptr;
   const EncodeJob* d_enc = nullptr;
@@ -312,8 +311,11 @@ struct th_lora {
   const NttJob* d_moe_ntt = nullptr;  // per batch and such limb: transform in place, Montgomery copy
   uint32_t moe_ntt_jobs = 0;
   // pinned host staging of host-I/O tokens (hidden states in, deltas and
-  // segment sums out), the same pages every token
+  // segment sums out), the same pages every token; mapped into the device's
+  // address space (io_dev), so the token's last kernel writes host deltas
+  // there itself instead of a device-to-host copy after it
   void* io_host = nullptr;
+  double* io_dev = nullptr;
   size_t io_bytes = 0;
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
@@ -2029,7 +2031,6 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->m = (uint64_t*)set->alloc(nb * 2 * P);
   double* dec_parts = (double*)set->alloc(nb * decode_parts_doubles(c->logn) * 8);
   set->sums = (double*)set->alloc((size_t)nb * cols * 8);
-  set->deltas = (double*)set->alloc(set->n_deltas * 8);
   {
     // sampler and combine jobs; seeds and the public key come with each launch
     std::vector<SampleJob> sj(ni);
@@ -2203,8 +2204,9 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   // its first pass) measured about twice the time of one staged through
   // pages used before.
   set->io_bytes = std::max((size_t)ni * d * 8, (size_t)(set->n_deltas + (uint64_t)nb * cols) * 8);
-  HIPCHK(hipHostMalloc(&set->io_host, set->io_bytes, hipHostMallocDefault));
+  HIPCHK(hipHostMalloc(&set->io_host, set->io_bytes, hipHostMallocMapped));
   memset(set->io_host, 0, set->io_bytes);
+  HIPCHK(hipHostGetDevicePointer(reinterpret_cast<void**>(&set->io_dev), set->io_host, 0));
   HIPCHK(hipStreamSynchronize(c->stream));
 }
 
@@ -2448,7 +2450,9 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
       HIPCHK(hipMemcpyAsync(set->hidden, set->io_host, hbytes, hipMemcpyHostToDevice, st));
       z = set->hidden;
     }
-    double* dout = deltas_on_device ? deltas : set->deltas;
+    // host deltas: B is applied straight into the set's mapped staging pages
+    // (visible to the host once the stream is idle), read out below
+    double* dout = deltas_on_device ? deltas : set->io_dev;
     if (ctx->host_sampler) {
       queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, true, BandArgs{nullptr, 0.0});
     } else {
@@ -2469,7 +2473,6 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     const size_t db = set->n_deltas * 8, ib = (size_t)nb * set->cols * 8;
     if (!deltas_on_device || inter) {
       char* hh = (char*)set->io_host;  // stream order: after the hidden states' copy
-      if (!deltas_on_device) HIPCHK(hipMemcpyAsync(hh, set->deltas, db, hipMemcpyDeviceToHost, st));
       if (inter) HIPCHK(hipMemcpyAsync(hh + db, set->sums, ib, hipMemcpyDeviceToHost, st));
       wait_stream(ctx);
       if (!deltas_on_device) memcpy(deltas, hh, db);
