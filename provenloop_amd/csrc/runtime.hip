@@ -317,6 +317,7 @@ struct th_lora {
   void* io_host = nullptr;
   double* io_dev = nullptr;
   size_t io_bytes = 0;
+  size_t io_in_off = 0;  // byte offset of the hidden states, past the deltas and sums
   void* alloc(size_t bytes) {
     void* p = ctx->pool.get(bytes);
     owned.push_back(p);
@@ -2203,7 +2204,8 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   // here: a token staged through fresh pinned pages (the context's ring on
   // its first pass) measured about twice the time of one staged through
   // pages used before.
-  set->io_bytes = std::max((size_t)ni * d * 8, (size_t)(set->n_deltas + (uint64_t)nb * cols) * 8);
+  set->io_in_off = ((size_t)(set->n_deltas + (uint64_t)nb * cols) * 8 + 255) & ~(size_t)255;
+  set->io_bytes = set->io_in_off + (size_t)ni * d * 8;
   HIPCHK(hipHostMalloc(&set->io_host, set->io_bytes, hipHostMallocMapped));
   memset(set->io_host, 0, set->io_bytes);
   HIPCHK(hipHostGetDevicePointer(reinterpret_cast<void**>(&set->io_dev), set->io_host, 0));
@@ -2217,6 +2219,13 @@ void free_lora(th_lora* set) {
   delete set;
   ctx_release(c);
 }
+
+// Host hidden states up to this size are read by the encoder from the set's
+// mapped staging pages instead of being copied to the device first: a single
+// delta's 12 KiB. The encoder reads all N FFT inputs, each hidden value about
+// N / d times (replicas and the mirrored half: 11 at d = 1536), which for the
+// 1.5B shape's 344 KiB would be several MB across PCIe.
+constexpr size_t HOST_INPUT_MAPPED_MAX = 32 * 1024;
 
 // Queue one token of the set (the body of th_lora_deltas): encrypt_pk of every
 // input z (device, n_in x d) with randomness from the device sampler (band
@@ -2442,13 +2451,20 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     if (!async && !ctx->pending.empty()) drain(ctx);
     const size_t hbytes = (size_t)ni * set->d * 8;
     hipStream_t st = ctx->stream;
-    // device-resident inputs are read where they are; host inputs go through one copy
+    // device-resident inputs are read where they are; host inputs go through
+    // the set's staging pages (free: every host-I/O call waits for its work),
+    // read there by the encoder itself when small, else copied to the device
+    // first
     const double* z = hidden;
     if (!hidden_on_device) {
-      // the set's staging buffer is free: every host-I/O call waits for its copies
-      memcpy(set->io_host, hidden, hbytes);
-      HIPCHK(hipMemcpyAsync(set->hidden, set->io_host, hbytes, hipMemcpyHostToDevice, st));
-      z = set->hidden;
+      char* in = (char*)set->io_host + set->io_in_off;
+      memcpy(in, hidden, hbytes);
+      if (hbytes <= HOST_INPUT_MAPPED_MAX) {
+        z = set->io_dev + set->io_in_off / 8;
+      } else {
+        HIPCHK(hipMemcpyAsync(set->hidden, in, hbytes, hipMemcpyHostToDevice, st));
+        z = set->hidden;
+      }
     }
     // host deltas: B is applied straight into the set's mapped staging pages
     // (visible to the host once the stream is idle), read out below
