@@ -84,17 +84,30 @@ __device__ __forceinline__ void dit_stages_reg(double* re, double* im, uint32_t 
 #pragma unroll
       for (uint32_t r = 0; r < 8; ++r)
         if (r < (1u << R)) x[r] = Cx{re[P(base | (r << s0))], im[P(base | (r << s0))]};
+      // The twiddle of x[r]'s pair at stage s0 + rb is selected by its
+      // position's bits below s0 + rb: lo + (g << s0), g = r mod 2^rb (base
+      // has no bits in [s0, s0 + R)). So the group needs 2^rb twiddles per
+      // stage, 7 in all, requested together before the first butterfly.
+      double twr[7], twi[7];  // stage rb's twiddle g at (1 << rb) - 1 + g
 #pragma unroll
       for (uint32_t rb = 0; rb < 3; ++rb) {
         if (rb >= R) break;
-        const uint32_t s = s0 + rb, half = 1u << s;
+#pragma unroll
+        for (uint32_t g = 0; g < (1u << rb); ++g) {
+          const uint32_t w = (1u << (s0 + rb)) - 1 + lo + (g << s0);
+          twr[(1u << rb) - 1 + g] = stage_re[w];
+          twi[(1u << rb) - 1 + g] = stage_im[w];
+        }
+      }
+#pragma unroll
+      for (uint32_t rb = 0; rb < 3; ++rb) {
+        if (rb >= R) break;
 #pragma unroll
         for (uint32_t r = 0; r < 8; ++r) {
           if (r >= (1u << R) || (r & (1u << rb))) continue;
-          // position of x[r] is base | (r << s0); its bits below s select the twiddle
-          const uint32_t k = (base | (r << s0)) & (half - 1);
+          const uint32_t ti = (1u << rb) - 1 + (r & ((1u << rb) - 1));
           Cx t0, t1;
-          dit(x[r], x[r | (1u << rb)], stage_re[half - 1 + k], stage_im[half - 1 + k], t0, t1);
+          dit(x[r], x[r | (1u << rb)], twr[ti], twi[ti], t0, t1);
           x[r] = t0;
           x[r | (1u << rb)] = t1;
         }
