@@ -281,6 +281,48 @@ def test_lora_set_sampler_in_encoder_launch_limit(n_in):
         _check(got[i:i + 1], got_sums[i:i + 1], exp, exp_sums)
 
 
+@pytest.mark.parametrize("n_in", [4, 5])
+def test_lora_set_host_io_paths(env, n_in):
+    """Host hidden states of 4 x 1024 doubles (32 KiB) are read by the encoder from the set's
+    mapped staging pages, 5 x 1024 are copied to the device first; host deltas are written into
+    the staging pages by the last kernel. Every combination of host and device input and output
+    gives the same deltas bit for bit, twice in a row."""
+    eng, ref, sk, pk, rsk, rpk = env
+    L = _lib.load()
+    rng = np.random.default_rng(500 + n_in)
+    d = 1024
+    H = np.ascontiguousarray(rng.normal(size=(n_in, d)) * 0.1)
+    proj = _projections(rng, n_in, d, ranks=[6] * n_in, d_outs=[33] * n_in)
+    ls = zero_moai.LoraSet(eng, n_in, proj)
+    seeds = np.arange(900, 900 + n_in, dtype=np.uint64)
+    hd, od = C.c_void_p(), C.c_void_p()
+    _lib.check(L.th_dev_alloc(eng._h, H.nbytes, C.byref(hd)))
+    _lib.check(L.th_dev_alloc(eng._h, ls.n_deltas * 8, C.byref(od)))
+    try:
+        _lib.check(L.th_memcpy_h2d(eng._h, hd, _lib.ptr(H), H.nbytes))
+        results = []
+        for _ in range(2):
+            for hin in (0, 1):
+                for hout in (0, 1):
+                    out = np.full(ls.n_deltas, np.nan)
+                    dst = out.ctypes.data if hout else od.value
+                    src = H.ctypes.data if hin else hd.value
+                    _lib.check(L.th_lora_deltas(eng._h, ls._h, pk._h, sk._h, src, 0 if hin else 1,
+                                                seeds.ctypes.data, 1, dst, 0 if hout else 1, None))
+                    eng.sync()
+                    if not hout:
+                        _lib.check(L.th_memcpy_d2h(eng._h, _lib.ptr(out), od, out.nbytes))
+                    results.append(out)
+        for r in results[1:]:
+            assert np.array_equal(results[0], r)
+        exp, _ = _oracle(ref, rpk, rsk, H[:1], seeds[:1], [(0, proj[0][1], proj[0][2])], True)
+        got0 = results[0][ls.offsets[0]:ls.offsets[1]]
+        assert np.linalg.norm(got0 - exp[0]) <= 1e-9 * max(1.0, np.linalg.norm(exp[0]))
+    finally:
+        _lib.check(L.th_dev_free(eng._h, hd))
+        _lib.check(L.th_dev_free(eng._h, od))
+
+
 def test_lora_set_crt_branch_after_rescale():
     """A chain whose last prime is 30-bit: the rescaled scale is ~2^50 > 1.5 * 2^40, so the
     decrypt takes the CRT branch over limbs 0 and 1 (ciphertext.rs:351)."""
