@@ -271,13 +271,31 @@ int th_lora_free(th_lora* set);
 /* n_deltas = sum of d_out (length of th_lora_deltas' output), n_batches =
  * number of plaintext batches, cols = segments per batch. Any may be NULL. */
 int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, uint32_t* cols);
+/* th_lora_deltas mode bits.
+ * TH_LORA_RESCALE: rescale each product before decrypting it
+ *   (ciphertext.rs:476-535), as the LoRA pass at BASELINE depth does.
+ * TH_LORA_SK_FUSED: the decryption-fused shortcut. Without it (the default)
+ *   the token runs the reference's client/server sequence
+ *   (inference_engine.py:1477-1482): encrypt_pk forms every limb of c0 and c1
+ *   of each input from the public key alone; ct x pt (fused into the rescale
+ *   with TH_LORA_RESCALE) forms every limb of each batch's product or
+ *   rescaled product without the secret key; then one batched decrypt reads
+ *   only what it decodes (limb 0, or limbs 0 and 1 in the CRT branch) with the
+ *   secret key. Those ciphertexts stay in the set's working memory until the
+ *   next token (th_lora_ct). With TH_LORA_SK_FUSED the token forms only the
+ *   limbs its decryptions read and uses the secret key inside the encryption
+ *   (c0 + c1 s on limb 0 replaces c0 and c1 there), so no complete ciphertext
+ *   exists at any point: a single-party shortcut with the same deltas bit for
+ *   bit, not the reference's architecture (no counterpart in the reference). */
+enum { TH_LORA_RESCALE = 1, TH_LORA_SK_FUSED = 2 };
 /* One token of the encrypted LoRA path for every projection of the set (the
  * engine's _he_lora_delta, inference_engine.py:1244-1392, for all layers at
  * once), entirely on the device: encrypt_pk of each input replicated into
  * cols segments and seeded with seeds[i] (host array); ct x pt with every
- * cached batch; rescale when do_rescale (the product is formed inside the
- * rescale's transforms); batched decrypt + decode with segment sums; then
- * delta_j = B_j @ intermediate_j.
+ * cached batch; rescale when mode has TH_LORA_RESCALE (the product is formed
+ * inside the rescale's transforms); batched decrypt + decode with segment
+ * sums; then delta_j = B_j @ intermediate_j. mode: TH_LORA_* bits above
+ * (0 and 1 keep the meaning of the earlier do_rescale flag).
  *   hidden: n_inputs x d doubles, device memory if hidden_on_device, else host.
  *   deltas: n_deltas doubles (projection j at offset sum_{k<j} d_out[k]),
  *           device memory if deltas_on_device, else host.
@@ -294,8 +312,19 @@ int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, ui
  * Otherwise it returns after one synchronisation of the stream and one
  * device-to-host copy. */
 int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
-                   int hidden_on_device, const uint64_t* seeds, int do_rescale, double* deltas,
-                   int deltas_on_device, double* inter);
+                   int hidden_on_device, const uint64_t* seeds, int mode, double* deltas, int deltas_on_device,
+                   double* inter);
+/* A copy, as a new ciphertext object, of one ciphertext that the set's last
+ * token formed (no counterpart in the reference, whose per-token objects are
+ * the TenSafeCiphertext values of _he_lora_delta, inference_engine.py:1272,
+ * :1311): which = TH_LORA_CT_INPUT, the encrypt_pk output of input `index`
+ * (L limbs, scale 2^40); TH_LORA_CT_PRODUCT, batch `index`'s product
+ * ct x pt (L limbs, scale 2^80), rescaled (L - 1 limbs) if the token had
+ * TH_LORA_RESCALE. Queued tokens are settled first. TH_ESTATE if the set has
+ * run no token yet or its last token had TH_LORA_SK_FUSED (which forms no
+ * complete ciphertext). */
+enum { TH_LORA_CT_INPUT = 0, TH_LORA_CT_PRODUCT = 1 };
+int th_lora_ct(th_ctx* ctx, th_lora* set, int which, uint32_t index, th_ct** out);
 
 /* ---------------------------------------------------------------- ciphertext objects */
 int th_ct_free(th_ct* ct);

@@ -21,6 +21,8 @@ TH_OK, TH_EINVAL, TH_EDEVICE, TH_ENOMEM, TH_ESTATE = 0, -1, -2, -3, -4
 TH_OPT_SAMPLER, TH_OPT_FORCE_SERIAL_SAMPLER, TH_OPT_SAMPLER_BAND, TH_OPT_RESCALE_DECRYPT = 1, 2, 3, 4
 TH_RD_AUTO, TH_RD_SPLIT, TH_RD_WHOLE = 0, 1, 2
 TH_SAMPLER_DEVICE, TH_SAMPLER_HOST = 0, 1
+TH_LORA_RESCALE, TH_LORA_SK_FUSED = 1, 2
+TH_LORA_CT_INPUT, TH_LORA_CT_PRODUCT = 0, 1
 
 VP = C.c_void_p
 SZ = C.c_size_t
@@ -73,6 +75,7 @@ _SIGS = {
     "th_lora_free": (I32, [VP]),
     "th_lora_info": (I32, [VP, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32)]),
     "th_lora_deltas": (I32, [VP, VP, VP, VP, VP, I32, VP, I32, VP, I32, VP]),
+    "th_lora_ct": (I32, [VP, VP, I32, U32, PVP]),
     "th_ct_free": (I32, [VP]),
     "th_ct_info": (I32, [VP, C.POINTER(U32), C.POINTER(C.c_double)]),
     "th_ct_download": (I32, [VP, VP, VP, VP]),

@@ -290,7 +290,7 @@ __device__ __forceinline__ void job_ops(const NttArgs& a, const NttJob& jb, uint
 // Calls f.template operator()<LD, ST>() for the (load, store) pair of a launch.
 // Only the pairs the engine issues are instantiated: forward (NONE | ENC,
 // NONE), (REDUCE, RESCALE), (REDUCE, MUL_RESCALE), (NONE, MONT); inverse
-// (NONE | MUL | MULM | DOT, NONE), (DOT | DOTM, SEGSUM).
+// (NONE | MUL | MULM | DOT | DOTM, NONE), (DOT | DOTM, SEGSUM).
 template <bool INV, class F>
 __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
   if constexpr (!INV) {
@@ -312,6 +312,7 @@ __host__ hipError_t with_ops(uint32_t load, uint32_t store, F&& f) {
     if (load == NTT_LOAD_MUL) return f.template operator()<NTT_LOAD_MUL, NTT_STORE_NONE>();
     if (load == NTT_LOAD_MULM) return f.template operator()<NTT_LOAD_MULM, NTT_STORE_NONE>();
     if (load == NTT_LOAD_DOT) return f.template operator()<NTT_LOAD_DOT, NTT_STORE_NONE>();
+    if (load == NTT_LOAD_DOTM) return f.template operator()<NTT_LOAD_DOTM, NTT_STORE_NONE>();
     return hipErrorInvalidValue;
   }
 }

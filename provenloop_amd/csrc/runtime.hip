@@ -184,7 +184,7 @@ struct AsyncToken {
   const th_sk* sk;
   const double* hidden;  // device
   std::vector<uint64_t> seeds;
-  int do_rescale;
+  int mode;              // TH_LORA_* bits
   double* deltas;        // device
   uint32_t flag_off;     // band flags of its inputs
 };
@@ -268,7 +268,7 @@ struct th_lora {
   int64_t* mvals = nullptr;    // n_in x N encoded messages m (i64)
   uint64_t* prep = nullptr;    // n_in x 3L x N
   uint64_t* cts = nullptr;     // n_in x 2L x N
-  uint64_t* work = nullptr;    // n_batches x 2L x N: the rescale's inverse transforms
+  uint64_t* work = nullptr;    // n_batches x 2 x N: the last limb of each product as coefficients (inverse transforms)
   uint64_t* res = nullptr;     // n_batches x 2 nl_r x N: the rescaled limbs the decryption reads
   uint64_t* m = nullptr;       // n_batches x 2 x N, decrypted coefficients
   double* sums = nullptr;      // n_batches x cols
@@ -294,6 +294,18 @@ struct th_lora {
   uint32_t inv_nr_jobs = 0, nl_n = 1;
   uint32_t nl_r = 1;  // limbs a rescaled product's decryption reads (1, or 2 for the CRT branch)
   const DecodeJob *d_dec_r = nullptr, *d_dec_n = nullptr;
+  // The complete pass (th_lora_deltas without TH_LORA_SK_FUSED): every limb of
+  // each input's ciphertext (encrypt jobs of all limbs), every limb of each
+  // batch's product or rescaled product in outs, then the batched decrypt of
+  // the limbs it reads.
+  uint64_t* outs = nullptr;                   // n_batches x 2L x N (rescaled: 2(L-1) limb-polys each)
+  const NttJob* d_enc_all = nullptr;          // encrypt transforms of every limb
+  const NttJob* d_fwd_all = nullptr;          // rescale forward jobs of limbs 0..L-2 into outs
+  const NttJob* d_seg_all = nullptr;          // decrypt + segment sums in one transform (limb-0 branch)
+  const NttJob *d_dot_all_r = nullptr, *d_dot_all_n = nullptr;  // decrypt transforms into m
+  uint32_t dot_all_r_jobs = 0, dot_all_n_jobs = 0;
+  const CtPtJob* d_ctpt = nullptr;            // products without a rescale
+  int last_mode = -1;                         // mode of the last token queued (th_lora_ct)
   const LoraBJob* d_bjobs = nullptr;
   uint32_t dot_r_jobs = 0;
   const double* seg_w = nullptr;  // segment weights, or null: decode the slots and sum them
@@ -944,18 +956,22 @@ bool segsum_in_transform(const th_ctx* c, uint32_t jobs, uint32_t cols) {
 }
 
 // Decrypt transforms (c0 + c1 s on limb 0, inverse NTT) whose epilogue writes
-// each job's segment sums to its dst.
+// each job's segment sums to its dst: launches of at most one round of
+// whole-polynomial workgroups (256 jobs), so that a job's sums do not depend
+// on how many jobs the batch has.
 void launch_dot_segsum(th_ctx* c, const NttJob* d_jobs, uint32_t n, const th_sk* sk, const double* W, uint32_t cols) {
   NttArgs a{};
   a.lc = c->d_lc;
-  a.jobs = d_jobs;
   a.load = NTT_LOAD_DOTM;
   a.store = NTT_STORE_SEGSUM;
   a.bc = c->d_bc;
   a.key = sk_montgomery(c, sk);
   a.segw = W;
   a.cols = cols;
-  HIPCHK(launch_ntt((int)c->logn, true, a, n, c->stream));
+  for (uint32_t off = 0; off < n; off += 256) {
+    a.jobs = d_jobs + off;
+    HIPCHK(launch_ntt((int)c->logn, true, a, std::min<uint32_t>(256, n - off), c->stream));
+  }
 }
 
 void queue_decrypt(OpScope& sc, const std::vector<CtView>& cts, const th_sk* sk, double* out_dev, double* seg_dev,
@@ -1911,9 +1927,21 @@ void queue_regate(OpScope& sc, th_lora* set) {
     ej[v].dst = set->ptm + (v / k) * L * N;  // the group's sums, transformed in place below
     ej[v].parts = parts + v * pd;
   }
-  HIPCHK(launch_encode(sc.up(ej), (uint32_t)nv, c->d_bc, c->d_twist_re, c->d_twist_im, c->d_stage_re, c->d_stage_im,
-                       c->logn, L, c->stream, nullptr, nullptr, nullptr, 0, BandArgs{nullptr, 0.0}, k,
-                       set->moe_limbs));
+  // the fold sums at most ENC_FOLD_MAX_LIMBS limbs per launch: longer chains
+  // encode once per group of limbs
+  const EncodeJob* d_ej = sc.up(ej);
+  uint32_t rest = set->moe_limbs;
+  while (rest) {
+    uint32_t group = 0;
+    for (uint32_t l = 0, n = 0; l < 32 && n < ENC_FOLD_MAX_LIMBS; ++l)
+      if (rest >> l & 1) {
+        group |= 1u << l;
+        ++n;
+      }
+    rest &= ~group;
+    HIPCHK(launch_encode(d_ej, (uint32_t)nv, c->d_bc, c->d_twist_re, c->d_twist_im, c->d_stage_re, c->d_stage_im,
+                         c->logn, L, c->stream, nullptr, nullptr, nullptr, 0, BandArgs{nullptr, 0.0}, k, group));
+  }
   launch_jobs_ntt(c, false, set->d_moe_ntt, set->moe_ntt_jobs, NTT_LOAD_NONE, nullptr, nullptr, NTT_STORE_MONT);
   HIPCHK(launch_moe_mix_b(set->bexp, set->d_moe_p, set->d_gates, set->n_proj, k, set->max_b_count, set->bmix,
                           c->stream));
@@ -2028,7 +2056,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->prep = (uint64_t*)set->alloc(ni * 3 * L * P);
   double* enc_parts = (double*)set->alloc(ni * encode_parts_doubles(c->logn) * 8);
   set->cts = (uint64_t*)set->alloc(ni * 2 * L * P);
-  set->work = (uint64_t*)set->alloc(nb * 2 * L * P);
+  set->work = (uint64_t*)set->alloc(nb * 2 * P);
   set->m = (uint64_t*)set->alloc(nb * 2 * P);
   double* dec_parts = (double*)set->alloc(nb * decode_parts_doubles(c->logn) * 8);
   set->sums = (double*)set->alloc((size_t)nb * cols * 8);
@@ -2056,19 +2084,17 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     set->apack = persist(set, packed);
     set->moe_b = moe_b;
     set->d_gates = (double*)set->alloc((size_t)set->n_proj * k * 8);
-    // A token reads the plaintexts' limbs 0..nl-1 (its decryptions) and L-1
-    // (a rescale), in Montgomery form, and the plain form of limbs 0..nl_r-1
-    // only in a rescale on the split kernels (its store's ct x pt): the
-    // regated plaintexts are formed on those limbs.
-    const uint32_t nl_pt = std::max(nl_n, nl_r);
-    set->moe_limbs = ((1u << nl_pt) - 1) | (1u << (L - 1));
+    // A complete token (ct x pt on every limb) reads every limb of the
+    // plaintexts in plain form (the rescale's store, the products) and limb
+    // L-1 in Montgomery form (the rescale's inverse loads); a fused token
+    // reads limbs 0..nl-1 and L-1 in Montgomery form: the regated plaintexts
+    // are formed on every limb, in both forms.
+    set->moe_limbs = L >= 32 ? ~0u : (1u << L) - 1;
     std::vector<NttJob> mj;
     for (uint32_t bt = 0; bt < nb; ++bt)
       for (uint32_t l = 0; l < L; ++l) {
-        if (!(set->moe_limbs >> l & 1)) continue;
         const size_t off = ((size_t)bt * L + l) * N;
-        const bool plain = L >= 2 && !fused_rd && l < nl_r;
-        mj.push_back(NttJob{set->ptm + off, set->ptm + off, plain ? set->pts + off : nullptr, nullptr, l, 0});
+        mj.push_back(NttJob{set->ptm + off, set->ptm + off, set->pts + off, nullptr, l, 0});
       }
     set->d_moe_ntt = persist(set, mj);
     set->moe_ntt_jobs = (uint32_t)mj.size();
@@ -2126,6 +2152,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     // it (the other limbs would be the same residues as th_encrypt_pk's).
     const uint32_t full = L >= 32 ? ~0u : (1u << L) - 1;
     const NttJob* all = persist(set, enc_jobs(full));
+    set->d_enc_all = all;
     auto plan = [&](uint32_t mask) {
       if (mask != full && encrypt_limbs_supported((int)c->logn))
         return std::make_pair(persist(set, enc_jobs(mask)), mask);
@@ -2140,7 +2167,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
     const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
     const uint64_t* pt = set->pts + (size_t)bt * L * N;
     const uint64_t* ptm = set->ptm + (size_t)bt * L * N;
-    uint64_t* w = set->work + (size_t)bt * 2 * L * N;
+    uint64_t* w = set->work + (size_t)bt * 2 * N;
     uint64_t* r = fused_rd ? nullptr : set->res + (size_t)bt * 2 * nl_r * N;
     uint64_t* mm = set->m + (size_t)bt * 2 * N;
     if (L >= 2) {
@@ -2197,9 +2224,56 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   set->inv_nr_jobs = (uint32_t)inv_nr.size();
   set->dot_r_jobs = (uint32_t)dot_r.size();
   set->d_dec_n = persist(set, dec_n);
+  {
+    // The complete pass: the encryptions form every limb of c0 and c1
+    // (d_enc_all); each batch's rescale forms every limb of the rescaled
+    // product in outs, after the inverse transforms of its last limb
+    // (d_inv_mul, the product in their loads): forward jobs of the last limb
+    // reduced modulo limbs 0..L-2, the product ct_l pt_l, the subtraction and
+    // the scaling in their stores (queue_rescale's algebra; inverse job i
+    // owns forward jobs i (L-1) .. i (L-1) + L-2); without a rescale each
+    // batch's product ct x pt is formed on every limb. The decryption reads
+    // limb 0 of each (limbs 0 and 1 in the CRT branch): one transform with c0
+    // + c1 s in its load and the segment sums in its epilogue where the
+    // whole-polynomial kernel serves (N <= 16384, at most 8 segments; in
+    // launches of one round of workgroups), else transforms into m and the
+    // segment-sum (or decode) kernels.
+    set->outs = (uint64_t*)set->alloc(nb * 2 * L * P);
+    std::vector<NttJob> fa, seg, dr, dn;
+    std::vector<CtPtJob> cp(nb);
+    for (uint32_t bt = 0; bt < nb; ++bt) {
+      const uint64_t* ct = set->cts + (size_t)batch_input[bt] * 2 * L * N;
+      const uint64_t* pt = set->pts + (size_t)bt * L * N;
+      uint64_t* o = set->outs + (size_t)bt * 2 * L * N;
+      uint64_t* mm = set->m + (size_t)bt * 2 * N;
+      if (L >= 2) {
+        const uint64_t* w = set->work + (size_t)bt * 2 * N;
+        for (uint32_t comp = 0; comp < 2; ++comp)
+          for (uint32_t l = 0; l + 1 < L; ++l)
+            fa.push_back(NttJob{w + (size_t)comp * N, o + (size_t)(comp * (L - 1) + l) * N,
+                                ct + (size_t)(comp * L + l) * N, pt + (size_t)l * N, l, 0});
+        for (uint32_t l = 0; l < nl_r; ++l)
+          dr.push_back(NttJob{o + (size_t)l * N, mm + (size_t)l * N, o + (size_t)(L - 1 + l) * N, nullptr, l, 0});
+        seg.push_back(NttJob{o, reinterpret_cast<uint64_t*>(set->sums + (size_t)bt * cols), o + (size_t)(L - 1) * N,
+                             nullptr, 0, 0, scale_r});
+      }
+      cp[bt] = CtPtJob{ct, ct + (size_t)L * N, pt, o, L, 0};
+      for (uint32_t l = 0; l < nl_n; ++l)
+        dn.push_back(NttJob{o + (size_t)l * N, mm + (size_t)l * N, o + (size_t)(L + l) * N, nullptr, l, 0});
+    }
+    if (L >= 2) {
+      set->d_fwd_all = persist(set, fa);
+      set->d_dot_all_r = persist(set, dr);
+      set->dot_all_r_jobs = (uint32_t)dr.size();
+      if (nl_r == 1 && segsum_in_transform(c, std::min<uint32_t>(nb, 256), cols)) set->d_seg_all = persist(set, seg);
+    }
+    set->d_ctpt = persist(set, cp);
+    set->d_dot_all_n = persist(set, dn);
+    set->dot_all_n_jobs = (uint32_t)dn.size();
+  }
   set->d_bjobs = persist(set, bj);
   if (cols <= SEGSUM_MAX_COLS) set->seg_w = seg_weights(c, d, cols);
-  if (set->d_dot_seg || set->d_rd) set->seg_p = seg_pairs(c, d);
+  if (set->d_dot_seg || set->d_rd || set->d_seg_all) set->seg_p = seg_pairs(c, d);
   // Host-I/O tokens stage through one pinned buffer of the set, written once
   // here: a token staged through fresh pinned pages (the context's ring on
   // its first pass) measured about twice the time of one staged through
@@ -2227,28 +2301,13 @@ void free_lora(th_lora* set) {
 // 1.5B shape's 344 KiB would be several MB across PCIe.
 constexpr size_t HOST_INPUT_MAPPED_MAX = 32 * 1024;
 
-// Queue one token of the set (the body of th_lora_deltas): encrypt_pk of every
-// input z (device, n_in x d) with randomness from the device sampler (band
-// flags `band`) or, with host_draw, drawn on the host with glibc; ct x pt
-// inside the rescale's transforms; decrypt with segment sums; B applied into
-// dout (device, n_deltas).
-void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* z,
-                 const uint64_t* seeds, int do_rescale, double* dout, bool host_draw, BandArgs band) {
+// The rest of a TH_LORA_SK_FUSED token after the encoder: only the limbs the
+// decryptions read, with the secret key inside the encryption (D = c0 + c1 s
+// on the decrypted limbs instead of c0 and c1) and the rescale fused into the
+// decryption; no complete ciphertext is formed.
+void queue_fused_rest(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, bool do_rescale) {
   const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
   hipStream_t st = ctx->stream;
-  // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the
-  // launch. When every input's seed fits one launch, the encoder's launch
-  // draws the randomness too (the sampler's workgroups beside the encoder's)
-  const bool sample_in_encode = !host_draw && ni <= SEEDS_PER_LAUNCH;
-  if (host_draw) {
-    OpScope sc(ctx);
-    upload_host_draws(sc, seeds, ni, set->u, set->e0, set->e1);
-  } else if (!sample_in_encode) {
-    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, false, band));
-  }
-  HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
-                       ctx->d_stage_im, ctx->logn, L, st, z, sample_in_encode ? set->d_sample : nullptr, seeds,
-                       ctx->force_serial, band));
   // D = c0 + c1 s, all the decryption reads of an input's limbs 0..nl-1
   // (k_key_dot, or formed by the encrypt row passes in place of those limbs
   // where they run): limb 0 before the fused rescale-decrypt, limbs
@@ -2324,7 +2383,94 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
   else
     HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
                          ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
+}
+
+// The rest of a complete token after the encoder: the reference's
+// client/server sequence (inference_engine.py:1477-1482). encrypt_pk forms
+// every limb of c0 and c1 of each input from the public key (ciphertext.rs:
+// 240-319), ct x pt and the rescale every limb of each batch's product
+// (ciphertext.rs:422-429, :476-535) without the secret key, into the set's
+// working memory; then the batched decrypt (ciphertext.rs:327-400) reads the
+// limbs it decodes with the secret key.
+void queue_complete_rest(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, bool do_rescale) {
+  const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in, nb = set->n_batches;
+  hipStream_t st = ctx->stream;
+  {
+    NttArgs ea{};
+    ea.lc = ctx->d_lc;
+    ea.jobs = set->d_enc_all;
+    ea.load = NTT_LOAD_ENC;
+    ea.bc = ctx->d_bc;
+    const uint32_t full = L >= 32 ? ~0u : (1u << L) - 1;
+    bool combined = false;
+    HIPCHK(launch_encrypt((int)ctx->logn, ea, ni, L, full, EncDot{}, pk_pairs(ctx, pk), set->cts, &combined, st));
+    if (!combined) HIPCHK(launch_encrypt_combine(set->d_comb, ni, ctx->d_bc, N, L, st, pk->d));
+  }
+  const DecodeJob* dec = nullptr;
+  if (do_rescale) {
+    // inverse transforms of the products' last limb (ct x pt in their loads),
+    // forward transforms of its reductions with the product, the subtraction
+    // and the scaling in their stores: every limb of each rescaled product
+    NttArgs ia{}, fa{};
+    ia.lc = fa.lc = ctx->d_lc;
+    ia.bc = fa.bc = ctx->d_bc;
+    ia.jobs = set->d_inv_mul;
+    ia.load = NTT_LOAD_MULM;
+    fa.jobs = set->d_fwd_all;
+    fa.load = NTT_LOAD_REDUCE;
+    fa.store = NTT_STORE_MUL_RESCALE;
+    fa.rc = ctx->d_rc + (size_t)L * L;
+    HIPCHK(launch_rescale((int)ctx->logn, ia, nb * 2, fa, nb * 2 * (L - 1), st));
+    if (set->d_seg_all) {
+      launch_dot_segsum(ctx, set->d_seg_all, nb, sk, set->seg_p, set->cols);
+    } else {
+      launch_jobs_ntt(ctx, true, set->d_dot_all_r, set->dot_all_r_jobs, NTT_LOAD_DOTM, nullptr,
+                      sk_montgomery(ctx, sk));
+      dec = set->d_dec_r;
+    }
+  } else {
+    HIPCHK(launch_ct_pt_mul(set->d_ctpt, nb, L, ctx->d_bc, N, st));
+    launch_jobs_ntt(ctx, true, set->d_dot_all_n, set->dot_all_n_jobs, NTT_LOAD_DOTM, nullptr, sk_montgomery(ctx, sk));
+    dec = set->d_dec_n;
+  }
+  if (dec) {
+    if (set->seg_w)
+      HIPCHK(launch_segsum(dec, nb, ctx->d_dc, set->seg_w, ctx->logn, set->cols, st));
+    else
+      HIPCHK(launch_decode(dec, nb, ctx->d_dc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                           ctx->d_stage_im, ctx->logn, set->d, set->cols, st));
+  }
+}
+
+// Queue one token of the set (the body of th_lora_deltas): encrypt_pk of every
+// input z (device, n_in x d) with randomness from the device sampler (band
+// flags `band`) or, with host_draw, drawn on the host with glibc; ct x pt
+// (inside the rescale's transforms with TH_LORA_RESCALE); decrypt with
+// segment sums; B applied into dout (device, n_deltas). mode: TH_LORA_* bits.
+void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* z,
+                 const uint64_t* seeds, int mode, double* dout, bool host_draw, BandArgs band) {
+  const uint32_t N = ctx->N, L = ctx->L, ni = set->n_in;
+  const bool do_rescale = (mode & TH_LORA_RESCALE) != 0;
+  hipStream_t st = ctx->stream;
+  // encrypt_pk of every input (ciphertext.rs:240-319); seeds travel with the
+  // launch. When every input's seed fits one launch, the encoder's launch
+  // draws the randomness too (the sampler's workgroups beside the encoder's)
+  const bool sample_in_encode = !host_draw && ni <= SEEDS_PER_LAUNCH;
+  if (host_draw) {
+    OpScope sc(ctx);
+    upload_host_draws(sc, seeds, ni, set->u, set->e0, set->e1);
+  } else if (!sample_in_encode) {
+    HIPCHK(launch_sample_pk(set->d_sample, ni, N, ctx->force_serial, st, seeds, true, false, band));
+  }
+  HIPCHK(launch_encode(set->d_enc, ni, ctx->d_bc, ctx->d_twist_re, ctx->d_twist_im, ctx->d_stage_re,
+                       ctx->d_stage_im, ctx->logn, L, st, z, sample_in_encode ? set->d_sample : nullptr, seeds,
+                       ctx->force_serial, band));
+  if (mode & TH_LORA_SK_FUSED)
+    queue_fused_rest(ctx, set, pk, sk, do_rescale);
+  else
+    queue_complete_rest(ctx, set, pk, sk, do_rescale);
   HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
+  set->last_mode = mode;
 }
 
 void resolve_pending(th_ctx* c) {
@@ -2344,7 +2490,7 @@ void resolve_pending(th_ctx* c) {
   // sampler, which reproduces their (unflagged) draws exactly
   for (size_t i = 0; i < redo.size(); ++i) {
     const AsyncToken& t = redo[i];
-    queue_token(c, t.set, t.pk, t.sk, t.hidden, t.seeds.data(), t.do_rescale, t.deltas, flagged[i] != 0,
+    queue_token(c, t.set, t.pk, t.sk, t.hidden, t.seeds.data(), t.mode, t.deltas, flagged[i] != 0,
                 BandArgs{nullptr, 0.0});
     if (flagged[i]) c->redrawn_inputs += t.set->n_in;
   }
@@ -2435,16 +2581,55 @@ int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, ui
   });
 }
 
+int th_lora_ct(th_ctx* ctx, th_lora* set, int which, uint32_t index, th_ct** out) {
+  return guarded([&] {
+    TH_LOCK(ctx);
+    need(set && set->ctx == ctx, "LoRA set belongs to another context");
+    need(out != nullptr, "null output");
+    need(which == TH_LORA_CT_INPUT || which == TH_LORA_CT_PRODUCT, "which must be TH_LORA_CT_INPUT or _PRODUCT");
+    // a queued token redone later (sampler band) rewrites these ciphertexts: settle first
+    if (!ctx->pending.empty()) drain(ctx);
+    need(set->last_mode >= 0, "the LoRA set has run no token yet", TH_ESTATE);
+    need(!(set->last_mode & TH_LORA_SK_FUSED),
+         "the set's last token ran with TH_LORA_SK_FUSED, which forms no complete ciphertext", TH_ESTATE);
+    const uint32_t L = ctx->L, N = ctx->N;
+    const uint64_t* src;
+    uint32_t limbs;
+    double scale;
+    if (which == TH_LORA_CT_INPUT) {
+      need(index < set->n_in, "input index out of range");
+      src = set->cts + (size_t)index * 2 * L * N;
+      limbs = L;
+      scale = kScale;
+    } else {
+      need(index < set->n_batches, "batch index out of range");
+      src = set->outs + (size_t)index * 2 * L * N;
+      const bool rs = (set->last_mode & TH_LORA_RESCALE) != 0;
+      limbs = rs ? L - 1 : L;
+      scale = rs ? kScale * kScale / (double)ctx->q[L - 1] : kScale * kScale;  // ciphertext.rs:427, :533
+    }
+    th_ct* ct = new_ct(ctx, limbs, scale);
+    const hipError_t e =
+        hipMemcpyAsync(ct->d, src, 2 * (size_t)limbs * poly_bytes(ctx), hipMemcpyDeviceToDevice, ctx->stream);
+    if (e != hipSuccess) {
+      drop(ct);
+      hipchk(e, "hipMemcpyAsync");
+    }
+    *out = ct;
+  });
+}
+
 int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,
-                   int hidden_on_device, const uint64_t* seeds, int do_rescale, double* deltas,
-                   int deltas_on_device, double* inter) {
+                   int hidden_on_device, const uint64_t* seeds, int mode, double* deltas, int deltas_on_device,
+                   double* inter) {
   return guarded([&] {
     TH_LOCK(ctx);
     need(set && set->ctx == ctx, "LoRA set belongs to another context");
     need(pk && pk->ctx == ctx && sk && sk->ctx == ctx, "keys belong to another context");
     need(hidden && seeds && deltas, "null argument");
     const uint32_t L = ctx->L, ni = set->n_in, nb = set->n_batches;
-    need(!do_rescale || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
+    need((mode & ~(TH_LORA_RESCALE | TH_LORA_SK_FUSED)) == 0, "unknown th_lora_deltas mode bits");
+    need(!(mode & TH_LORA_RESCALE) || L >= 2, "Cannot rescale: only 1 limb left", TH_ESTATE);
     const bool async = hidden_on_device && deltas_on_device && !inter;
     // tokens queued asynchronously before are settled first, so that a redo
     // of one of them cannot overwrite this call's results
@@ -2470,18 +2655,18 @@ int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, 
     // (visible to the host once the stream is idle), read out below
     double* dout = deltas_on_device ? deltas : set->io_dev;
     if (ctx->host_sampler) {
-      queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, true, BandArgs{nullptr, 0.0});
+      queue_token(ctx, set, pk, sk, z, seeds, mode, dout, true, BandArgs{nullptr, 0.0});
     } else {
       const uint32_t off = take_flags(ctx, ni);
-      queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, false, band_args(ctx, off));
+      queue_token(ctx, set, pk, sk, z, seeds, mode, dout, false, band_args(ctx, off));
       if (async) {
         ctx->pending.push_back(
-            AsyncToken{set, pk, sk, z, std::vector<uint64_t>(seeds, seeds + ni), do_rescale, deltas, off});
+            AsyncToken{set, pk, sk, z, std::vector<uint64_t>(seeds, seeds + ni), mode, deltas, off});
         return;
       }
       wait_stream(ctx);
       if (any_flag(ctx, off, ni)) {  // a draw in the band: the token again, from glibc draws
-        queue_token(ctx, set, pk, sk, z, seeds, do_rescale, dout, true, BandArgs{nullptr, 0.0});
+        queue_token(ctx, set, pk, sk, z, seeds, mode, dout, true, BandArgs{nullptr, 0.0});
         ctx->redrawn_inputs += ni;
       }
       release_flags(ctx, off);

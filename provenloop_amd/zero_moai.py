@@ -31,7 +31,7 @@ from typing import Dict, List, Sequence
 import numpy as np
 
 from . import _lib
-from .tensafe_he import CkksContext, TenSafePlaintext, TenSafePublicKey, TenSafeSecretKey
+from .tensafe_he import CkksContext, TenSafeCiphertext, TenSafePlaintext, TenSafePublicKey, TenSafeSecretKey
 
 
 def layout(simd_slots: int, d_model: int, rank: int):
@@ -218,9 +218,19 @@ class LoraSet:
             raise ValueError(f"gates must be [{len(self.d_out)}, {self.n_experts}]")
         _lib.check(self._lib.th_lora_set_gates(self._ctx._h, self._h, _lib.ptr(G)))
 
+    @staticmethod
+    def _mode(rescale: bool, sk_fused: bool) -> int:
+        return (_lib.TH_LORA_RESCALE if rescale else 0) | (_lib.TH_LORA_SK_FUSED if sk_fused else 0)
+
     def deltas(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden, seeds, rescale: bool = True,
-               with_intermediates: bool = False):
-        """Host in, host out: hidden [n_inputs, d] -> list of per-projection deltas."""
+               with_intermediates: bool = False, sk_fused: bool = False):
+        """Host in, host out: hidden [n_inputs, d] -> list of per-projection deltas.
+
+        By default the token forms every ciphertext of the reference's
+        client/server sequence (encrypt_pk, ct x pt and rescale without the
+        secret key; the batched decrypt reads only what it decodes).
+        sk_fused=True takes the single-party shortcut (TH_LORA_SK_FUSED): the
+        same deltas bit for bit, no complete ciphertext formed."""
         H = np.ascontiguousarray(hidden, np.float64)
         if H.shape != (self.n_inputs, self.d):
             raise ValueError(f"hidden must be [{self.n_inputs}, {self.d}]")
@@ -230,13 +240,13 @@ class LoraSet:
         out = np.empty(self.n_deltas, np.float64)
         inter = np.empty((self.n_batches, self.cols), np.float64) if with_intermediates else None
         _lib.check(self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk),
-                                            _lib.ptr(H), 0, _lib.ptr(sd), int(bool(rescale)), _lib.ptr(out), 0,
+                                            _lib.ptr(H), 0, _lib.ptr(sd), self._mode(rescale, sk_fused), _lib.ptr(out), 0,
                                             None if inter is None else _lib.ptr(inter)))
         parts = [out[self.offsets[j]:self.offsets[j + 1]] for j in range(len(self.d_out))]
         return (parts, inter) if with_intermediates else parts
 
     def deltas_device(self, pk: TenSafePublicKey, sk: TenSafeSecretKey, hidden_dev: int, seeds, dev_out: int,
-                      rescale: bool = True):
+                      rescale: bool = True, sk_fused: bool = False):
         """Device in, device out: hidden_dev points at n_inputs x d doubles in
         HBM, dev_out receives n_deltas doubles. Only queues the token on the
         context stream (no host synchronisation): call ctx.sync(), or order
@@ -247,6 +257,16 @@ class LoraSet:
         # plain ints for the pointer arguments (the binding declares them
         # c_void_p): this call is on the per-token path
         rc = self._lib.th_lora_deltas(self._ctx._h, self._h, self._ctx._own(pk), self._ctx._own(sk), hidden_dev, 1,
-                                      sd.ctypes.data, 1 if rescale else 0, dev_out, 1, None)
+                                      sd.ctypes.data, self._mode(rescale, sk_fused), dev_out, 1, None)
         if rc:
             _lib.check(rc)
+
+    def ciphertext(self, which: str, index: int) -> TenSafeCiphertext:
+        """A copy of a ciphertext the last token formed (th_lora_ct): which =
+        "input" (the encrypt_pk output of input `index`) or "product" (batch
+        `index`'s ct x pt, rescaled if the token rescaled). Raises
+        RuntimeError after a sk_fused token, which forms none."""
+        w = {"input": _lib.TH_LORA_CT_INPUT, "product": _lib.TH_LORA_CT_PRODUCT}[which]
+        out = C.c_void_p()
+        _lib.check(self._lib.th_lora_ct(self._ctx._h, self._h, w, int(index), C.byref(out)))
+        return TenSafeCiphertext(out, self._ctx)

@@ -21,3 +21,17 @@ def orc():
     if not os.path.exists(o._LIB_PATH):
         o.build()
     return o
+
+
+@pytest.fixture(params=["complete", "sk_fused"])
+def lora_mode(request, monkeypatch):
+    """Runs a LoRA-set test in both token modes: the complete pass (every
+    ciphertext of the reference's client/server sequence formed) and the
+    sk-fused shortcut (TH_LORA_SK_FUSED). The mode is set for every
+    LoraSet.deltas / deltas_device call of the test."""
+    if request.param == "sk_fused":
+        from provenloop_amd import zero_moai
+
+        mode = zero_moai.LoraSet._mode
+        monkeypatch.setattr(zero_moai.LoraSet, "_mode", staticmethod(lambda rescale, sk_fused: mode(rescale, True)))
+    return request.param

@@ -19,7 +19,7 @@ import pytest
 from oracle import oracle as orc
 from provenloop_amd import _lib, tensafe_he, zero_moai
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("lora_mode")]
 
 
 @pytest.fixture(scope="module")

@@ -14,7 +14,7 @@ import pytest
 from oracle import oracle as orc
 from provenloop_amd import tensafe_he, zero_moai
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("lora_mode")]
 
 K = 3  # experts per projection
 
@@ -193,3 +193,43 @@ def test_moe_set_gates_errors(env):
     plain = zero_moai.LoraSet(eng, 1, [(0, proj[0][1][0], proj[0][2][0])])
     with pytest.raises(RuntimeError, match="without gates"):
         plain.set_gates(np.ones((1, 1)))
+
+
+def test_moe_full_shape_two_tokens(env):
+    """The full CryptoMOE shape: 28 layers x {q, v} x 3 rank-16 experts (224 batches, 672 expert
+    encodes per regate), two successive tokens each with its own gates (th_lora_set_gates) and
+    device-resident inputs and outputs; layers 0 and 27 of both tokens against the oracle's
+    literal k products + ct_add + rescale + decrypt with that token's gates."""
+    import ctypes as C
+
+    from provenloop_amd import _lib
+
+    eng, ref, sk, pk, rsk, rpk = env
+    lib = _lib.load()
+    rng = np.random.default_rng(28)
+    proj, g0 = _experts(rng, 28)
+    ls = zero_moai.LoraSet(eng, 28, proj, gates=g0)
+    assert ls.n_batches == 224
+    hd, od = C.c_void_p(), C.c_void_p()
+    _lib.check(lib.th_dev_alloc(eng._h, 28 * 1536 * 8, C.byref(hd)))
+    _lib.check(lib.th_dev_alloc(eng._h, ls.n_deltas * 8, C.byref(od)))
+    try:
+        for t in range(2):
+            H = np.ascontiguousarray(rng.normal(size=(28, 1536)) * 0.1)
+            gt = np.array([zero_moai.softmax_gate(5000 * t + j, K) for j in range(len(proj))])
+            seeds = [700 + 50 * t + i for i in range(28)]
+            _lib.check(lib.th_memcpy_h2d(eng._h, hd, _lib.ptr(H), H.nbytes))
+            ls.set_gates(gt)
+            ls.deltas_device(pk, sk, hd.value, seeds, od.value)
+            eng.sync()
+            out = np.empty(ls.n_deltas)
+            _lib.check(lib.th_memcpy_d2h(eng._h, _lib.ptr(out), od, ls.n_deltas * 8))
+            for l in (0, 27):
+                sub = [(0, A, B) for _, A, B in proj[2 * l:2 * l + 2]]
+                exp, _ = _oracle(ref, rpk, rsk, H[l:l + 1], seeds[l:l + 1], sub, gt[2 * l:2 * l + 2])
+                for j, e in zip((2 * l, 2 * l + 1), exp):
+                    g = out[ls.offsets[j]:ls.offsets[j + 1]]
+                    assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e), (t, l, j)
+    finally:
+        _lib.check(lib.th_dev_free(eng._h, hd))
+        _lib.check(lib.th_dev_free(eng._h, od))

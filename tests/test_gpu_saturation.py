@@ -3,11 +3,13 @@ chain: NTT, encrypt_pk, ct x pt, rescale and decrypt bit-exact against the
 oracle on that chain, and LoRA sets (q, k, v, o at rank 32, hidden 3584)
 serving several sessions, each with its own keys, on one context.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from provenloop_amd import tensafe_he, zero_moai
+from provenloop_amd import _lib, tensafe_he, zero_moai
 from provenloop_amd.params import CHAIN_N32768_L8
 
 pytestmark = pytest.mark.gpu
@@ -79,6 +81,7 @@ def _oracle_deltas(ref, rpk, rsk, H, seeds, proj):
     return out
 
 
+@pytest.mark.usefixtures("lora_mode")
 def test_saturation_sessions_match_oracle(ctxs):
     """One layer of q/k/v/o (rank 32: 8 batches of 4 rows each) for two sessions with their own
     keys, hidden states and seeds, served by one LoRA set."""
@@ -99,20 +102,50 @@ def test_saturation_sessions_match_oracle(ctxs):
             assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e)
 
 
+@pytest.mark.usefixtures("lora_mode")
 def test_saturation_full_layer_count(ctxs):
-    """All 28 layers (56 inputs, 112 projections, 896 products of 8 limbs) in one set; the last
-    layer's q and o projections against the oracle, and the device-resident run equal to it."""
+    """All 28 layers (56 inputs, 112 projections, 896 products of 8 limbs) in one set serving two
+    sessions (own keys, hidden states and seeds) queued back to back with device-resident inputs
+    and outputs and one synchronisation: each session's layer-27 q and o projections against the
+    oracle, and the second session's host-I/O run equal to its device-resident one."""
     eng, ref = ctxs
+    lib = _lib.load()
     rng = np.random.default_rng(6)
     proj = _layer_projections(rng, 28)
     ls = zero_moai.LoraSet(eng, 56, proj)
     assert ls.n_batches == 896
-    sk, rsk = eng.keygen(seed=7), ref.keygen(7)
-    pk, rpk = eng.keygen_public(sk, seed=8), ref.keygen_public(rsk, 8)
-    H = rng.normal(size=(56, D)) * 0.1
-    seeds = list(range(500, 556))
-    got = ls.deltas(pk, sk, H, seeds)
+    sess = []
+    for s in range(2):
+        sk, rsk = eng.keygen(seed=7 + 10 * s), ref.keygen(7 + 10 * s)
+        pk, rpk = eng.keygen_public(sk, seed=8 + 10 * s), ref.keygen_public(rsk, 8 + 10 * s)
+        H = np.ascontiguousarray(rng.normal(size=(56, D)) * 0.1)
+        sess.append((sk, pk, rsk, rpk, H, list(range(500 + 100 * s, 556 + 100 * s))))
+    bufs = []
+    try:
+        for sk, pk, _, _, H, seeds in sess:
+            hd, od = C.c_void_p(), C.c_void_p()
+            _lib.check(lib.th_dev_alloc(eng._h, H.nbytes, C.byref(hd)))
+            bufs.append(hd)
+            _lib.check(lib.th_dev_alloc(eng._h, ls.n_deltas * 8, C.byref(od)))
+            bufs.append(od)
+            _lib.check(lib.th_memcpy_h2d(eng._h, hd, _lib.ptr(H), H.nbytes))
+        eng.sync()
+        for s, (sk, pk, _, _, H, seeds) in enumerate(sess):
+            ls.deltas_device(pk, sk, bufs[2 * s].value, seeds, bufs[2 * s + 1].value)
+        eng.sync()
+        outs = []
+        for s in range(2):
+            out = np.empty(ls.n_deltas)
+            _lib.check(lib.th_memcpy_d2h(eng._h, _lib.ptr(out), bufs[2 * s + 1], ls.n_deltas * 8))
+            outs.append(out)
+    finally:
+        for b in bufs:
+            _lib.check(lib.th_dev_free(eng._h, b))
     last = [(0 if i == 54 else 1, A, B) for i, A, B in (proj[108], proj[111])]
-    exp = _oracle_deltas(ref, rpk, rsk, H[54:56], seeds[54:56], last)
-    for g, e in zip((got[108], got[111]), exp):
-        assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e)
+    for s, (sk, pk, rsk, rpk, H, seeds) in enumerate(sess):
+        exp = _oracle_deltas(ref, rpk, rsk, H[54:56], seeds[54:56], last)
+        for j, e in zip((108, 111), exp):
+            g = outs[s][ls.offsets[j]:ls.offsets[j + 1]]
+            assert np.linalg.norm(g - e) <= 1e-3 * np.linalg.norm(e), (s, j)
+    sk, pk, _, _, H, seeds = sess[1]
+    assert np.array_equal(np.concatenate(ls.deltas(pk, sk, H, seeds)), outs[1])
