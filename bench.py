@@ -3,24 +3,36 @@
 
 Step = one per-token HE-LoRA pass at Qwen2.5-1.5B shape, N = 16384, the
 reference's 4-limb chain, scale 2^40: 28 layers x {q, v} projections
-(hidden 1536, rank 16, B_q [1536,16], B_v [256,16]). Per token: 28
-encrypt_pk of the replicated layer inputs, 224 column-packed ct x pt
-products (4 batches per projection), each rescaled and decrypted with
-segment sums, then B @ intermediate, all on the GPU (one LoRA-set call, one
-stream synchronisation; the pass forms the limbs its decryptions read, and
-its deltas are those of the full sequence). Hidden states are in HBM before
-the timed region starts and the deltas stay in HBM; the same pass with host
-inputs and outputs is reported beside it as pcie_inclusive. 56 encrypted
-LoRA deltas per token; value = deltas/s. Order on the GPU: the roofline
-microbench, the warm-up tokens, the pipelined and the reference-sequence
-tokens, the timed tokens, the host-I/O tokens, then the other figures.
+(hidden 1536, rank 16, B_q [1536,16], B_v [256,16]). Per token, the
+reference's client/server sequence (inference_engine.py:1477-1482): 28
+encrypt_pk of the replicated layer inputs, each forming every limb of c0 and
+c1 from the public key; 224 column-packed ct x pt products (4 batches per
+projection), each fused into a rescale that forms every limb of the
+rescaled product, without the secret key; then one batched decrypt that
+reads limb 0 of each product with the secret key and writes segment sums;
+then B @ intermediate; all on the GPU (one LoRA-set call, one stream
+synchronisation). Hidden states are in HBM before the timed region starts
+and the deltas stay in HBM; the same pass with host inputs and outputs is
+reported beside it as pcie_inclusive. 56 encrypted LoRA deltas per token;
+value = deltas/s. The input ciphertexts and rescaled products of layers 0
+and 27 of the last timed token are copied out of the set (th_lora_ct) and
+compared with the oracle bit for bit. Order on the GPU: the roofline
+microbench, the warm-up tokens, the pipelined, reference-sequence and
+sk-fused tokens, the timed tokens, the host-I/O tokens, then the other
+figures.
 
 Also measured in the same run:
   * roofline: the batched NTT (64 polynomials x 4 limbs, N = 16384, forward
-    and inverse as separate launches), timed with HIP events on the engine's
-    stream before the token passes; algorithmic bytes = read + write of
-    every limb-polynomial; the same round trip at N = 32768 (reference chain
-    for that degree) is reported beside it as ntt_n32768;
+    and inverse as separate launches, coefficients range_u64(q_l) from one
+    seeded ChaCha20 stream in (polynomial, limb, coefficient) order), timed
+    with HIP events on the engine's stream before the token passes;
+    algorithmic bytes = read + write of every limb-polynomial; the same
+    round trip at N = 32768 (reference chain for that degree) is reported
+    beside it as ntt_n32768;
+  * sk_fused: the same tokens through the single-party shortcut
+    (TH_LORA_SK_FUSED: only the limbs the decryptions read, the secret key
+    inside the encryption, no complete ciphertext); reported beside value,
+    never as it;
   * single_delta: the latency of one encrypted LoRA delta (encrypt_pk, 4
     column-packed ct x pt, rescale, decrypt to 16 floats), host in and out;
   * moe: the CryptoMOE variant with a gate that changes every token (3
@@ -72,6 +84,70 @@ def seeds_for(token):
     return [1_000_003 * token + l + 1 for l in range(LAYERS)]
 
 
+# ------------------------------------------------------------------ seeded inputs
+NTT_SEED = 2024
+
+
+def _chacha_blocks(seed, first, count):
+    """ChaCha20 blocks first .. first+count-1 of TenSafeRng::from_seed(seed)
+    (rng.rs:38-68, :163-206: key words (lo, hi) x 4, block counter in word
+    12, nonce 0), as a [count, 16] uint32 array."""
+    lo, hi = seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF
+    st = np.zeros((16, count), np.uint32)
+    st[0:4] = np.array([0x61707865, 0x3320646E, 0x79622D32, 0x6B206574], np.uint32)[:, None]
+    st[4:12:2], st[5:12:2] = lo, hi
+    st[12] = (np.arange(first, first + count, dtype=np.uint64) & 0xFFFFFFFF).astype(np.uint32)
+    w = st.copy()
+
+    def rotl(x, r):
+        return (x << np.uint32(r)) | (x >> np.uint32(32 - r))
+
+    def qr(a, b, c, d):
+        w[a] += w[b]; w[d] ^= w[a]; w[d] = rotl(w[d], 16)
+        w[c] += w[d]; w[b] ^= w[c]; w[b] = rotl(w[b], 12)
+        w[a] += w[b]; w[d] ^= w[a]; w[d] = rotl(w[d], 8)
+        w[c] += w[d]; w[b] ^= w[c]; w[b] = rotl(w[b], 7)
+
+    for _ in range(10):
+        qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15)
+        qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14)
+    return (w + st).T
+
+
+def seeded_residues(seed, moduli, polys, n):
+    """[polys, len(moduli), n] uint64: coefficient (p, l, i) = range_u64(q_l) of
+    one TenSafeRng::from_seed(seed) stream, drawn in (p, l, i) order
+    (rng.rs:99-103 next_u64 = lo | hi << 32; rng.rs:124-133 rejects
+    r < (2^64 - q) % q and returns r % q)."""
+    q = np.asarray(moduli, np.uint64)
+    L = q.size
+    total = polys * L * n
+    mods = np.broadcast_to(np.repeat(q, n)[None, :], (polys, L * n)).reshape(-1)
+    thr = np.array([((1 << 64) - int(x)) % int(x) for x in q], np.uint64)
+    thr_seq = np.broadcast_to(np.repeat(thr, n)[None, :], (polys, L * n)).reshape(-1)
+    blocks = (total + 7) // 8  # 8 u64 per block
+    words = _chacha_blocks(seed, 0, blocks).reshape(-1).astype(np.uint64)
+    r = words[0::2] | (words[1::2] << np.uint64(32))
+    r = r[:total]
+    if not np.any(r < thr_seq):
+        return (r % mods).reshape(polys, L, n)
+    # a rejection shifts every later draw: consume the stream one draw at a time
+    out = np.empty(total, np.uint64)
+    pos, have, blk = 0, r, blocks
+    for k in range(total):
+        while True:
+            if pos >= have.size:
+                more = _chacha_blocks(seed, blk, 64).reshape(-1).astype(np.uint64)
+                have = np.concatenate([have, more[0::2] | (more[1::2] << np.uint64(32))])
+                blk += 64
+            x = have[pos]
+            pos += 1
+            if x >= thr_seq[k]:
+                out[k] = x % mods[k]
+                break
+    return out.reshape(polys, L, n)
+
+
 # ------------------------------------------------------------------ GPU side
 def gpu_setup(A, B):
     from provenloop_amd import tensafe_he, zero_moai
@@ -104,9 +180,9 @@ class DeviceInputs:
         _lib.check(self.L.th_memcpy_h2d(ctx._h, self.h, _lib.ptr(Hs), Hs.nbytes))
         ctx.sync()
 
-    def run(self, pk, sk, step, seeds, rescale=True):
+    def run(self, pk, sk, step, seeds, rescale=True, sk_fused=False):
         self.lora.deltas_device(pk, sk, self.h.value + step * self.h_stride, seeds, self.o.value + step * self.o_stride,
-                                rescale=rescale)
+                                rescale=rescale, sk_fused=sk_fused)
 
     def deltas(self, step):
         from provenloop_amd import _lib
@@ -135,8 +211,8 @@ class NttRoofline:
         self.ctx, self.L = ctx, _lib.load()
         self.q = ctx.moduli[:4]
         self.n = ctx.poly_mod_degree
-        rng = np.random.default_rng(2)
-        self.host = np.stack([rng.integers(0, qq, (64, self.n), dtype=np.uint64) for qq in self.q], axis=1)
+        self.seed = NTT_SEED
+        self.host = seeded_residues(self.seed, self.q, 64, self.n)
         self.dev = C.c_void_p()
         _lib.check(self.L.th_dev_alloc(ctx._h, self.host.nbytes, C.byref(self.dev)))
         _lib.check(self.L.th_memcpy_h2d(ctx._h, self.dev, _lib.ptr(self.host), self.host.nbytes))
@@ -177,6 +253,7 @@ class NttRoofline:
         per_launch = 2 * nbytes  # read + write of every limb-polynomial
         return {
             "polys": 64, "limbs": 4, "N": self.n, "bytes_per_launch": per_launch,
+            "input": f"range_u64(q_l) of TenSafeRng::from_seed({self.seed}), (polynomial, limb, coefficient) order",
             "fwd_ms": f, "inv_ms": i,
             "fwd_GBs": per_launch / (f * 1e-3) / 1e9, "inv_GBs": per_launch / (i * 1e-3) / 1e9,
             "roundtrip_ms": f + i, "roundtrip_GBs": 2 * per_launch / ((f + i) * 1e-3) / 1e9,
@@ -204,6 +281,29 @@ def ntt_traffic():
     k = p["calibration"]["factor"]
     per = [(p[d]["fetch_kib"] + p[d]["write_kib"]) * 1024 * k for d in ("forward", "inverse")]
     return int(sum(per) / len(per))
+
+
+def roofline_block(ntt):
+    """The line's roofline object for the batched NTT. `bound` names the
+    resource closer to saturation by the committed counters: "hbm" when the
+    achieved share of 8 TB/s is at least the VALU-busy share, else "valu"
+    (VALU issue; there is no MFMA work)."""
+    frac = ntt["roundtrip_GBs"] / HBM_PEAK_GBS
+    valu = ntt_valu_busy()
+    bound = "hbm" if valu is None or frac >= valu else "valu"
+    return {
+        "kernel": "ntt (batched forward + inverse, 64 polys x 4 limbs, N=16384)",
+        "bound": bound,
+        "achieved": round(ntt["roundtrip_GBs"], 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(frac, 4),
+        "traffic": ntt_traffic(),
+        "valu_busy": valu,
+        "limiter": "neither HBM nor VALU saturated: per CU the loads, the 60-bit limbs' integer arithmetic, "
+                   "the LDS exchanges and the stores follow one another (one polynomial per CU at this "
+                   "batch); bound = the larger of the HBM and VALU-busy shares; no MFMA work",
+    }
 
 
 def ntt_valu_busy():
@@ -410,18 +510,18 @@ def ntt_only(chain="default", n=N):
 
 
 # ------------------------------------------------------------------ secondary workloads
-def _timed_sessions(ctx, lora, sessions, dev_by_session, steps, warmup, seeds_fn):
+def _timed_sessions(ctx, lora, sessions, dev_by_session, steps, warmup, seeds_fn, sk_fused=False):
     """Time `steps` steps; a step queues one token of every session (its own keys,
     HBM-resident inputs and outputs) and synchronises the stream once."""
     for w in range(warmup):
         for s, (pk, sk) in enumerate(sessions):
-            dev_by_session[s].run(pk, sk, steps + w, seeds_fn(s, 10_000 + w))
+            dev_by_session[s].run(pk, sk, steps + w, seeds_fn(s, 10_000 + w), sk_fused=sk_fused)
     ctx.sync()
     seeds = {(s, t): np.asarray(seeds_fn(s, t), np.uint64) for s in range(len(sessions)) for t in range(steps)}
     t0 = time.perf_counter()
     for t in range(steps):
         for s, (pk, sk) in enumerate(sessions):
-            dev_by_session[s].run(pk, sk, t, seeds[(s, t)])
+            dev_by_session[s].run(pk, sk, t, seeds[(s, t)], sk_fused=sk_fused)
         ctx.sync()
     return time.perf_counter() - t0
 
@@ -472,6 +572,13 @@ def moe_workload(steps, warmup):
     elapsed = time.perf_counter() - t0
     last = steps - 1
     flat = dev.deltas(last)
+    t1 = time.perf_counter()
+    for t in range(steps):
+        lora.set_gates(gates[t])
+        dev.run(pk, sk, t, seeds[t], sk_fused=True)
+        ctx.sync()
+    fused_elapsed = time.perf_counter() - t1
+    fused_equal = bool(np.array_equal(dev.deltas(last), flat))
     dev.free()
     ref = orc.Context(N)
     rsk = ref.keygen(11)
@@ -502,8 +609,11 @@ def moe_workload(steps, warmup):
         "workload": "CryptoMOE per-token pass, Qwen2.5-1.5B shape: 28 layers x {q,v} x 3 rank-16 experts, a "
                     "softmax gate per projection drawn for every token; per token the gate-scaled expert "
                     "plaintexts are encoded, transformed and folded on the device (th_lora_set_gates), then "
-                    "encrypt_pk, one product per batch (the ct_add of the experts' products, bit for bit), "
-                    "rescale, one batched decrypt; hidden states and deltas resident in HBM",
+                    "encrypt_pk (every limb), one product per batch (the ct_add of the experts' products, bit "
+                    "for bit) fused into a rescale that forms every limb, one batched decrypt of limb 0; hidden "
+                    "states and deltas resident in HBM",
+        "sk_fused": {"value": round(deltas / fused_elapsed, 3), "ms_per_step": round(fused_elapsed / steps * 1e3, 4),
+                     "deltas_equal": fused_equal},
         "parity": {"delta_rel_err_max_layer0": max(rel)},
     }
 
@@ -550,7 +660,12 @@ def saturation_workload(steps, warmup, parity_checks=((0, 4 * 27), (0, 4 * 27 + 
     def seeds_fn(s, t):
         return [(7_000_003 * s + 1_000_003 * t + i + 1) % (1 << 63) for i in range(2 * layers)]
 
+    fused_elapsed = _timed_sessions(ctx, lora, keys, devs, steps, warmup, seeds_fn, sk_fused=True)
+    fused_last = devs[0].deltas(steps - 1)
     elapsed = _timed_sessions(ctx, lora, keys, devs, steps, warmup, seeds_fn)
+    complete_last = devs[0].deltas(steps - 1)
+    # at N = 32768 the two modes sum each decryption's segments in different orders
+    fused_rel = float(np.max(np.abs(complete_last - fused_last)) / np.max(np.abs(complete_last)))
     ref = orc.Context(n, CHAIN_N32768_L8)
     S, cols = n // 2, (n // 2) // d
     last = steps - 1
@@ -578,9 +693,13 @@ def saturation_workload(steps, warmup, parity_checks=((0, 4 * 27), (0, 4 * 27 + 
         "ms_per_step": round(elapsed / steps * 1e3, 4),
         "session_tokens_per_s": round(sessions * steps / elapsed, 3),
         "workload": "32 concurrent sessions, Qwen2.5-7B shape: 28 layers x {q,k,v,o}, hidden 3584, rank 32 "
-                    "(8 batches of 4 rows), N=32768, 8-limb chain, scale 2^40; per session token 56 encrypt_pk, "
-                    "896 ct x pt + rescale, one batched decrypt; all sessions queued as one batch per step with "
-                    "one host synchronisation",
+                    "(8 batches of 4 rows), N=32768, 8-limb chain, scale 2^40; per session token 56 encrypt_pk "
+                    "(every limb), 896 ct x pt fused into rescales that form every limb (7), one batched decrypt "
+                    "of limb 0; all sessions queued as one batch per step with one host synchronisation",
+        "sk_fused": {"value": round(per_step * steps / fused_elapsed, 3),
+                     "ms_per_step": round(fused_elapsed / steps * 1e3, 4),
+                     "max_rel_diff_session0": fused_rel,
+                     "note": "the shortcut sums each decryption's segments in another order at N=32768"},
         "sessions": sessions, "N": n, "moduli": CHAIN_N32768_L8,
         "parity": {"delta_rel_err_max": max(rel), "checked": [list(c) for c in parity_checks]},
     }
@@ -610,12 +729,17 @@ def single_delta_workload(ctx, sk, pk, cpu, reps=100, warm=10):
     h = (rng.normal(size=D) * 0.1).astype(np.float32).astype(np.float64)
     lora = zero_moai.LoraSet(ctx, 1, [(0, A, np.eye(RANK))])  # B = I: the deltas are the 16 intermediates
     H = h[None]
-    times = []
-    for t in range(warm + reps):
-        t0 = time.perf_counter()
-        out = lora.deltas(pk, sk, H, [50_000 + t])
-        times.append(time.perf_counter() - t0)
-    lat = float(np.median(times[warm:]))
+
+    def latency(sk_fused):
+        times = []
+        for t in range(warm + reps):
+            t0 = time.perf_counter()
+            out = lora.deltas(pk, sk, H, [50_000 + t], sk_fused=sk_fused)
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times[warm:])), out
+
+    lat_f, out_f = latency(True)
+    lat, out = latency(False)
     S, cols = N // 2, (N // 2) // D
     t0 = time.perf_counter()
     rct = cpu.ctx.encrypt_pk(zero_moai.replicate(h, S, D), cpu.pk, 50_000 + warm + reps - 1)
@@ -629,8 +753,11 @@ def single_delta_workload(ctx, sk, pk, cpu, reps=100, warm=10):
     return {
         "latency_ms": round(lat * 1e3, 4), "deltas_per_s": round(1.0 / lat, 3), "reps": reps, "warmup": warm,
         "workload": "one encrypted LoRA delta, N=16384, 4-limb chain, scale 2^40: encrypt_pk of the replicated "
-                    "1536-dim hidden state, 4 ct x pt with cached plaintexts of LoRA-A [16,1536], rescale, "
-                    "decrypt with segment sums -> 16 floats; host input and output, one synchronisation",
+                    "1536-dim hidden state (every limb, public key only), 4 ct x pt with cached plaintexts of "
+                    "LoRA-A [16,1536] fused into rescales that form every limb of each product, decrypt of limb 0 "
+                    "with segment sums -> 16 floats; host input and output, one synchronisation",
+        "sk_fused_latency_ms": round(lat_f * 1e3, 4),
+        "sk_fused_equal": bool(np.array_equal(out[0], out_f[0])),
         "cpu_oracle_ms_1thread": round(cpu_ms, 2),
         "cpu_oracle_note": "the same delta on the CPU oracle, one host thread, plaintext encoding included "
                            "(the reference's Python path encodes uncached)",
@@ -743,6 +870,14 @@ def main():
     norescale_elapsed = time.perf_counter() - t3
     flat_nr = dev.deltas(args.steps - 1)
 
+    # the single-party shortcut (TH_LORA_SK_FUSED): reported beside value, never as it
+    t4 = time.perf_counter()
+    for t in range(args.steps):
+        dev.run(pk, sk, t, seed_arr[t], sk_fused=True)
+        ctx.sync()
+    fused_elapsed = time.perf_counter() - t4
+    flat_fused = dev.deltas(args.steps - 1)
+
     tok = []
     t0 = time.perf_counter()
     for t in range(args.steps):
@@ -753,6 +888,16 @@ def main():
     deltas_per_token = LAYERS * 2
     value = deltas_per_token * args.steps / elapsed
     tok_ms = np.diff(np.concatenate([[t0], tok])) * 1e3
+    flat_timed = dev.deltas(args.steps - 1)
+    # the ciphertexts the last timed token formed: the encrypt_pk output of
+    # layers 0 and 27 and their 8 rescaled products each (copies queued now,
+    # before any other token reuses the set's working memory)
+    check_layers = (0, LAYERS - 1)
+    timed_cts = {("input", l): lora.ciphertext("input", l) for l in check_layers}
+    for l in check_layers:
+        for j, p in enumerate("qv"):
+            for b in range(4):
+                timed_cts[(p, l, b)] = lora.ciphertext("product", (2 * l + j) * 4 + b)
 
     # the same pass with host inputs and outputs (PCIe included): reported beside value
     t1 = time.perf_counter()
@@ -772,12 +917,19 @@ def main():
     cpu = CpuLayer(A, B)
     hs, sd = hidden[last], seeds[last]
     rel, rel_nr = [], []
-    for l in (0, LAYERS - 1):
-        ref, _, _ = cpu.run(l, hs[l], sd[l])
+    n_ct_checked, n_ct_exact = 0, 0
+    for l in check_layers:
+        ref, r_prods, r_in = cpu.run(l, hs[l], sd[l])
         for j, p in enumerate("qv"):
             k = 2 * l + j
             g, c = flat[lora.offsets[k]:lora.offsets[k + 1]], ref[p]
             rel.append(float(np.linalg.norm(g - c) / np.linalg.norm(c)))
+        pairs = [(timed_cts[("input", l)], r_in)] + [(timed_cts[(p, l, b)], r_prods[(p, b)]) for p in "qv"
+                                                     for b in range(4)]
+        for g_ct, r_ct in pairs:
+            n_ct_checked += 1
+            n_ct_exact += int(g_ct.num_limbs == r_ct.num_limbs and g_ct.scale == r_ct.scale and all(
+                np.array_equal(x, y) for x, y in zip(ctx.ct_download(g_ct), cpu.ctx.ct_data(r_ct))))
     ref_nr, _, _ = cpu.run(0, hs[0], sd[0], rescale=False)
     for j, p in enumerate("qv"):
         g, c = flat_nr[lora.offsets[j]:lora.offsets[j + 1]], ref_nr[p]
@@ -801,12 +953,16 @@ def main():
     ntt32 = ntt_roofline(ctx32)
     del ctx32
 
+    # the timed token's deltas equal the host-I/O token's and the shortcut's (same residues)
+    timed_equal_fused = bool(np.array_equal(flat_timed, flat_fused))
+    timed_equal_host = bool(np.array_equal(flat_timed, flat))
+
     extra = {}
     if not args.no_extra:
         extra["single_delta"] = single_delta_workload(ctx, sk, pk, cpu)
         del lora
         extra["moe"] = moe_workload(steps=10, warmup=2)
-        extra["saturation"] = saturation_workload(steps=3, warmup=1, parity_checks=((0, 4 * 27),))
+        extra["saturation"] = saturation_workload(steps=3, warmup=1)
 
     if args.no_cpu:
         cpu_single = cpu_multi = None
@@ -830,25 +986,15 @@ def main():
         "data": "synthetic (seeded N(0,1)*0.1 hidden states, N(0,0.02) LoRA A/B, random-init)",
         "config": {
             "workload": "per-token HE-LoRA pass, Qwen2.5-1.5B shape: 28 layers x {q,v}, hidden 1536, rank 16, "
-                        "N=16384, 4-limb chain [60,40,40,60], scale 2^40, 4 ct x pt batches per projection, "
-                        "rescale, one batched decrypt per token, B @ intermediate on the GPU; hidden states "
-                        "and deltas resident in HBM, one host synchronisation per token",
+                        "N=16384, 4-limb chain [60,40,40,60], scale 2^40; the reference's client/server sequence: "
+                        "28 encrypt_pk (every limb of c0 and c1, public key only), 224 column-packed ct x pt fused "
+                        "into rescales that form every limb of each product (no secret key), one batched decrypt "
+                        "of limb 0 per token (secret key), B @ intermediate on the GPU; hidden states and deltas "
+                        "resident in HBM, one host synchronisation per token",
             "N": N, "layers": LAYERS, "hidden": D, "rank": RANK, "deltas_per_token": deltas_per_token,
             "tokens_per_s": round(args.steps / elapsed, 3),
         },
-        "roofline": {
-            "kernel": "ntt (batched forward + inverse, 64 polys x 4 limbs, N=16384)",
-            "bound": "hbm",
-            "achieved": round(ntt["roundtrip_GBs"], 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(ntt["roundtrip_GBs"] / HBM_PEAK_GBS, 4),
-            "traffic": ntt_traffic(),
-            "valu_busy": ntt_valu_busy(),
-            "limiter": "neither HBM nor VALU saturated: per CU the loads, the 60-bit limbs' integer "
-                       "arithmetic, the LDS exchanges and the stores follow one another (one polynomial "
-                       "per CU at this batch); no MFMA work",
-        },
+        "roofline": roofline_block(ntt),
         "token_ms": {"median": round(float(np.median(tok_ms)), 4), "first": round(float(tok_ms[0]), 4),
                      "last": round(float(tok_ms[-1]), 4), "min": round(float(tok_ms.min()), 4)},
         "reference_sequence": {
@@ -858,6 +1004,15 @@ def main():
                         "ct x pt, then decrypt without a rescale (scale 2^80: the CRT branch over limbs 0 and 1), "
                         "segment sums, B @ intermediate; one host synchronisation per token",
             "parity": {"delta_rel_err_max_layer0": max(rel_nr)},
+        },
+        "sk_fused": {
+            "value": round(deltas_per_token * args.steps / fused_elapsed, 3), "unit": "deltas/s",
+            "ms_per_step": round(fused_elapsed / args.steps * 1e3, 4),
+            "workload": "the same tokens through the single-party shortcut (TH_LORA_SK_FUSED): only the limbs the "
+                        "decryptions read, c0 + c1 s formed with the secret key inside the encryption, the rescale "
+                        "fused into the decryption; no complete ciphertext exists, so a server without the secret "
+                        "key cannot run it; not the reference's architecture and never the value",
+            "deltas_equal_complete_pass": timed_equal_fused,
         },
         "pipelined": {
             "value": round(deltas_per_token * args.steps / piped, 3), "unit": "deltas/s",
@@ -874,6 +1029,11 @@ def main():
                            frac=round(ntt32["roundtrip_GBs"] / HBM_PEAK_GBS, 4)),
         "parity": {
             "delta_rel_err_max": max(rel),
+            "timed_pass_ciphertexts_bitexact": n_ct_exact == n_ct_checked,
+            "timed_pass_ciphertexts_checked": f"{n_ct_exact} of {n_ct_checked} bit-exact: the encrypt_pk output "
+                                              f"(4 limbs) and the 8 rescaled products (3 limbs) of layers 0 and 27 "
+                                              f"of the last timed token, copied out of the set (th_lora_ct)",
+            "timed_deltas_equal_host_io": timed_equal_host,
             "device_io_equals_host_io": dev_host_equal,
             "encrypt_pk_bitexact": bool(ct_exact),
             "ctpt_rescale_bitexact": bool(rs_exact),

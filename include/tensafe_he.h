@@ -87,7 +87,7 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
  *   TH_SAMPLER_HOST - the host draws them exactly as the reference does.
  * TH_OPT_FORCE_SERIAL_SAMPLER: 1 makes the device sampler replay every
  *   stream serially (the path taken after a range_u32 rejection); testing only.
- * TH_OPT_SAMPLER_BAND: v in [-52, -1], default -36: the device sampler flags
+ * TH_OPT_SAMPLER_BAND: v in [-40, -1], default -36: the device sampler flags
  *   every Gaussian draw whose z * 3.19 lies within 2^v of a rounding boundary
  *   k + 1/2 (where the device's log/cos could round differently from glibc's;
  *   their difference stays below about 2^-45), and such an input's randomness
@@ -95,10 +95,12 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
  *   the reference's in every case. Calls that return results check the flags
  *   before returning (th_encrypt_pk and th_encrypt_pk_batch therefore wait for
  *   their work); tokens th_lora_deltas queues without waiting are checked at
- *   the next th_ctx_sync, th_memcpy_d2h, th_lora_free or synchronising call,
- *   which queues a flagged token again (and, in order, the tokens queued after
- *   it) before returning. A wider band only makes the host redraw more often
- *   (tests use it to exercise that path).
+ *   the next th_ctx_sync, th_memcpy_h2d, th_memcpy_d2h, th_dev_free,
+ *   th_lora_free or synchronising call, which queues a flagged token again
+ *   (and, in order, the tokens queued after it) before returning. A wider
+ *   band only makes the host redraw more often (tests use it to exercise that
+ *   path); bands below 2^-40 would come within 2^5 of the largest
+ *   device-glibc difference and are refused.
  * TH_OPT_RESCALE_DECRYPT: which kernels LoRA sets created afterwards use to
  *   rescale and decrypt their products: TH_RD_AUTO (default) - one workgroup
  *   per product from 160 to 256 batches at N <= 16384 (and at every batch
@@ -303,12 +305,15 @@ enum { TH_LORA_RESCALE = 1, TH_LORA_SK_FUSED = 2 };
  * With hidden and deltas in device memory and inter == NULL the call only
  * queues the token's kernels on the context stream and returns (no host
  * synchronisation; order later work with th_ctx_stream / th_ctx_sync). The
- * device input, the output buffer and the keys must then stay valid until the
- * next th_ctx_sync (or th_memcpy_d2h): if a Gaussian draw of the token landed
- * in the sampler's band (TH_OPT_SAMPLER_BAND) that call queues the token again
- * from glibc draws. Work the caller orders after the token on the stream sees
- * its first result; read the deltas after th_ctx_sync to have them exact in
- * every case.
+ * device input, the output buffer and the keys must then stay unchanged (and
+ * allocated) until the next th_ctx_sync; th_memcpy_h2d, th_memcpy_d2h and
+ * th_dev_free settle queued tokens first. If a Gaussian draw of the token
+ * landed in the sampler's band (TH_OPT_SAMPLER_BAND), the token writes NaN
+ * for every delta of the projections that read that input, and the settling
+ * call queues the token again from glibc draws, which overwrites them: work
+ * the caller orders after the token on the stream sees the exact deltas or
+ * NaN, never another value; read the deltas after th_ctx_sync to have them
+ * exact in every case.
  * Otherwise it returns after one synchronisation of the stream and one
  * device-to-host copy. */
 int th_lora_deltas(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, const double* hidden,

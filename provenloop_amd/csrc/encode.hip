@@ -152,7 +152,7 @@ __global__ __launch_bounds__(SAMPLE_ENC_THREADS) void k_sample_encode_parts(
   }
   const SampleJob jb = sample[blockIdx.y];
   const uint64_t seed = job_seed(jb, sb, use_sb, blockIdx.y);
-  uint8_t* flag = band.flags ? band.flags + blockIdx.y : nullptr;
+  const FlagOut flag = flag_of(band, blockIdx.y);
   const uint32_t b0 = (blockIdx.x - P) * SPT * SAMPLE_ENC_THREADS + threadIdx.x;
 #pragma unroll 1
   for (int k = 0; k < SPT; ++k) sample_block(jb, seed, 1u << logn, b0 + k * SAMPLE_ENC_THREADS, band.band, flag);
@@ -241,8 +241,7 @@ __global__ __launch_bounds__(256) void k_encode_final(const EncodeJob* __restric
   // no thread of this kernel reads the randomness being rewritten)
   if (fix && blockIdx.x == 0 && threadIdx.x == 0) {
     const SampleJob sj = fix[blockIdx.y];
-    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial,
-                   band.flags ? band.flags + blockIdx.y : nullptr, band.band);
+    sample_fix_job(sj, job_seed(sj, sb, use_sb, blockIdx.y), n, force_serial, flag_of(band, blockIdx.y), band.band);
   }
   const uint32_t M = n >> LP;
   const EncodeJob jb = jobs[blockIdx.y];

@@ -28,11 +28,33 @@ constexpr uint32_t SEEDS_PER_LAUNCH = 64;
 // memory; null for none) is set to 1 when a Gaussian draw of job j lands
 // within `band` of a rounding boundary (near_rounding_boundary), where the
 // device's log/cos could round differently from glibc's. The host then
-// redraws that job's randomness with glibc.
+// redraws that job's randomness with glibc. With dflags, dflags[j] (device
+// memory) is set to gen as well, for kernels later on the stream that check a
+// job's flag without a read across PCIe (a value left by an earlier launch
+// holds an older generation, so the array needs no clearing).
 struct BandArgs {
   uint8_t* flags;
   double band;
+  uint32_t* dflags = nullptr;
+  uint32_t gen = 0;
 };
+// The flags of launch `b` from job `first` on.
+inline BandArgs band_from(const BandArgs& b, uint32_t first) {
+  return BandArgs{b.flags ? b.flags + first : nullptr, b.band, b.dflags ? b.dflags + first : nullptr, b.gen};
+}
+// One job's band-flag outputs (FlagOut::raise sets both).
+struct FlagOut {
+  uint8_t* host;
+  uint32_t* dev;
+  uint32_t gen;
+  __device__ void raise() const {
+    if (host) *host = 1;
+    if (dev) *dev = gen;
+  }
+};
+__device__ inline FlagOut flag_of(const BandArgs& b, uint32_t j) {
+  return FlagOut{b.flags ? b.flags + j : nullptr, b.dflags ? b.dflags + j : nullptr, b.gen};
+}
 // Default band: 2^-36, about 2^9 times the largest difference between the
 // device's and glibc's z * 3.19.
 constexpr double SAMPLER_BAND_DEFAULT = 0x1p-36;

@@ -58,12 +58,12 @@ struct LoraBJob {
   uint32_t d_out;
   uint32_t rank;
   uint32_t first_row;  // first plaintext batch of the projection
-  uint32_t pad_;
+  uint32_t input;      // the input the projection reads (its band flag)
   uint64_t out_off;    // offset of the projection's deltas in the output
 };
 
 hipError_t launch_lora_b(const LoraBJob* jobs, uint32_t njobs, uint32_t max_d_out, const double* sums, double* out,
-                         uint32_t cols, hipStream_t s);
+                         uint32_t cols, hipStream_t s, const uint32_t* flags = nullptr, uint32_t gen = 0);
 
 // One plaintext batch of a mixture LoRA set: its projection and how many of
 // its slots hold A rows (rows x d).

@@ -219,6 +219,11 @@ struct th_ctx {
   uint8_t* bflag_host = nullptr;
   uint8_t* bflag_dev = nullptr;
   uint32_t bflag_cap = 0, bflag_used = 0;
+  // The same flags in device memory as generations (BandArgs::dflags): a
+  // token's kernels read them there instead of across PCIe; band_gen numbers
+  // the calls that sample.
+  uint32_t* bflag_gen = nullptr;
+  uint32_t band_gen = 0;
   std::vector<AsyncToken> pending;
   uint64_t redrawn_inputs = 0;  // inputs whose randomness was drawn again on the host (th_ctx_stats)
   std::unordered_set<void*> user_allocs;  // th_dev_alloc buffers not yet freed
@@ -536,7 +541,14 @@ bool any_flag(const th_ctx* c, uint32_t off, uint32_t n) {
   return false;
 }
 
-BandArgs band_args(const th_ctx* c, uint32_t off) { return BandArgs{c->bflag_dev + off, c->band}; }
+// The band flags of one sampling call (a new generation for the device copy).
+BandArgs band_args(th_ctx* c, uint32_t off) {
+  if (++c->band_gen == 0) {  // the generations wrapped: clear the device copy
+    HIPCHK(hipMemsetAsync(c->bflag_gen, 0, (size_t)c->bflag_cap * 4, c->stream));
+    c->band_gen = 1;
+  }
+  return BandArgs{c->bflag_dev + off, c->band, c->bflag_gen + off, c->band_gen};
+}
 
 // The public key as prepared pairs, made on the context's stream the first
 // time it is needed (queued before its first reader).
@@ -723,7 +735,7 @@ void destroy_ctx(th_ctx* c) {
   c->pool.release_all();
   c->ring.destroy();
   void* bufs[] = {c->d_lc, c->d_bc, c->d_q, c->d_rc, c->d_dc, c->d_twist_re, c->d_twist_im,
-                  c->d_stage_re, c->d_stage_im, c->d_tables};
+                  c->d_stage_re, c->d_stage_im, c->d_tables, c->bflag_gen};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
@@ -1250,6 +1262,8 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       c->bflag_cap = 1u << 16;
       HIPCHK(hipHostMalloc((void**)&c->bflag_host, c->bflag_cap, hipHostMallocMapped | hipHostMallocCoherent));
       HIPCHK(hipHostGetDevicePointer((void**)&c->bflag_dev, c->bflag_host, 0));
+      HIPCHK(hipMalloc((void**)&c->bflag_gen, (size_t)c->bflag_cap * 4));
+      HIPCHK(hipMemset(c->bflag_gen, 0, (size_t)c->bflag_cap * 4));
     } catch (...) {
       destroy_ctx(c);
       throw;
@@ -1527,7 +1541,7 @@ int th_ctx_set_option(th_ctx* ctx, int option, int64_t value) {
         ctx->force_serial = value != 0;
         break;
       case TH_OPT_SAMPLER_BAND:
-        need(value >= -52 && value <= -1, "sampler band must be 2^v for v in [-52, -1]");
+        need(value >= -40 && value <= -1, "sampler band must be 2^v for v in [-40, -1]");
         ctx->band = std::ldexp(1.0, (int)value);
         break;
       case TH_OPT_RESCALE_DECRYPT:
@@ -1984,7 +1998,7 @@ void build_lora(th_lora* set, const uint32_t* input_of, const uint32_t* ranks, c
   uint64_t out_off = 0, boff = 0;
   for (uint32_t j = 0; j < set->n_proj; ++j) {
     const uint32_t nb = (ranks[j] + cols - 1) / cols;
-    bj[j] = LoraBJob{nullptr, d_out[j], ranks[j], (uint32_t)batch_input.size(), 0, out_off};
+    bj[j] = LoraBJob{nullptr, d_out[j], ranks[j], (uint32_t)batch_input.size(), input_of[j], out_off};
     for (uint32_t bt = 0; bt < nb; ++bt) {
       const uint32_t rows = std::min(cols, ranks[j] - bt * cols);
       for (uint32_t x = 0; x < k; ++x) {
@@ -2469,7 +2483,8 @@ void queue_token(th_ctx* ctx, th_lora* set, const th_pk* pk, const th_sk* sk, co
     queue_fused_rest(ctx, set, pk, sk, do_rescale);
   else
     queue_complete_rest(ctx, set, pk, sk, do_rescale);
-  HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st));
+  HIPCHK(launch_lora_b(set->d_bjobs, set->n_proj, set->max_d_out, set->sums, dout, set->cols, st, band.dflags,
+                       band.gen));
   set->last_mode = mode;
 }
 
@@ -2840,7 +2855,9 @@ int th_dev_alloc(th_ctx* ctx, size_t bytes, void** out) {
 int th_dev_free(th_ctx* ctx, void* p) {
   return guarded([&] {
     TH_LOCK(ctx);
-    need(ctx->user_allocs.erase(p) == 1, "pointer was not allocated by th_dev_alloc, or was already freed");
+    need(ctx->user_allocs.count(p) == 1, "pointer was not allocated by th_dev_alloc, or was already freed");
+    if (!ctx->pending.empty()) drain(ctx);  // a queued token redone later may read this buffer
+    ctx->user_allocs.erase(p);
     ctx->pool.put(p);
   });
 }
@@ -2848,6 +2865,7 @@ int th_dev_free(th_ctx* ctx, void* p) {
 int th_memcpy_h2d(th_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return guarded([&] {
     TH_LOCK(ctx);
+    if (!ctx->pending.empty()) drain(ctx);  // a queued token redone later may read what this overwrites
     HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
   });

@@ -28,7 +28,7 @@ __global__ void k_sample_blocks(const SampleJob* __restrict__ jobs, uint32_t n, 
                                 BandArgs band) {
   const SampleJob jb = jobs[blockIdx.y];
   sample_block(jb, job_seed(jb, sb, use_sb, blockIdx.y), n, blockIdx.x * blockDim.x + threadIdx.x, band.band,
-               band.flags ? band.flags + blockIdx.y : nullptr);
+               flag_of(band, blockIdx.y));
 }
 
 // One workgroup per job: re-derive the u words; if any was rejected (== 0),
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_sample_check(const SampleJob* __restric
   }
   bad = __syncthreads_or(bad) | force_serial;
   if (!bad || threadIdx.x != 0) return;
-  serial_replay(jb, seed, n, band.flags ? band.flags + blockIdx.x : nullptr, band.band);
+  serial_replay(jb, seed, n, flag_of(band, blockIdx.x), band.band);
 }
 
 // One thread per job with a reject flag: replay flagged (or forced) jobs
@@ -56,7 +56,7 @@ __global__ void k_sample_fix(const SampleJob* __restrict__ jobs, uint32_t njobs,
   const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= njobs) return;
   const SampleJob jb = jobs[j];
-  sample_fix_job(jb, job_seed(jb, sb, use_sb, j), n, force_serial, band.flags ? band.flags + j : nullptr, band.band);
+  sample_fix_job(jb, job_seed(jb, sb, use_sb, j), n, force_serial, flag_of(band, j), band.band);
 }
 
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
@@ -69,7 +69,7 @@ hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, i
     const uint32_t cnt = njobs - first < SEEDS_PER_LAUNCH ? njobs - first : SEEDS_PER_LAUNCH;
     if (seeds)
       for (uint32_t i = 0; i < cnt; ++i) sb.v[i] = seeds[first + i];
-    const BandArgs bf{band.flags ? band.flags + first : nullptr, band.band};
+    const BandArgs bf = band_from(band, first);
     hipLaunchKernelGGL(k_sample_blocks, dim3((nblocks + 255) / 256, cnt), dim3(256), 0, s, jobs + first, n, sb,
                        seeds != nullptr, bf);
     if (flagged && fix_later)

@@ -69,9 +69,9 @@ static __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t
 // Block b (one ChaCha20 block of 16 words) of job jb's stream: the u values
 // of words [16 b, 16 b + 16) while they lie below n, else four Gaussian draws
 // (g = (16 b - n) / 4 onwards, e0 then e1). A zero u word sets the job's
-// reject flag; a draw within `band` of a rounding boundary sets *flag.
+// reject flag; a draw within `band` of a rounding boundary raises `flag`.
 static __device__ __forceinline__ void sample_block(const SampleJob& jb, uint64_t seed, uint32_t n, uint32_t b,
-                                                    double band, uint8_t* flag) {
+                                                    double band, const FlagOut& flag) {
   if (b >= 9 * (n / 16)) return;
   uint32_t w[16];
   chacha20((uint32_t)seed, (uint32_t)(seed >> 32), b, w);
@@ -97,7 +97,7 @@ static __device__ __forceinline__ void sample_block(const SampleJob& jb, uint64_
       else
         gst(jb.e1)[g - n] = e;
     }
-    if (any && flag) *flag = 1;  // a plain store; rare
+    if (any) flag.raise();  // plain stores; rare
   }
 }
 
@@ -127,8 +127,9 @@ struct SerialStream {
 
 // The reference's consumption order for one stream, walked serially
 // (handles range_u32 rejections: rng.rs:109-133, ciphertext.rs:255-273).
-// flag: this job's band flag (null: none).
-static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_t n, uint8_t* flag, double band) {
+// flag: this job's band flag outputs.
+static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_t n, const FlagOut& flag,
+                                     double band) {
   SerialStream st(seed);
   for (uint32_t i = 0; i < n; ++i) {
     uint32_t r = st.next();
@@ -146,14 +147,14 @@ static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_
     else
       jb.e1[i - n] = e;
   }
-  if (any && flag) *flag = 1;
+  if (any) flag.raise();
 }
 
 // The end of a flagged sampler launch for job j: replay the stream serially
 // if a u word was rejected (or force_serial), then clear the flag. Run by one
 // thread, in a launch ordered after the block kernel.
-static __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial, uint8_t* flag,
-                                      double band) {
+static __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial,
+                                      const FlagOut& flag, double band) {
   if (*jb.reject || force_serial) serial_replay(jb, seed, n, flag, band);
   *jb.reject = 0;
 }

@@ -20,7 +20,7 @@ from provenloop_amd import _lib, tensafe_he, zero_moai
 pytestmark = pytest.mark.gpu
 
 N = 8192
-WIDE, NARROW, DEFAULT = -4, -52, -36  # log2 of the band: nearly every input / none / the default
+WIDE, NARROW, DEFAULT = -4, -40, -36  # log2 of the band: nearly every input / (almost) none / the default
 
 
 @pytest.fixture(scope="module")
@@ -40,7 +40,7 @@ def _same_ct(eng, ref, ct, rct):
 
 def test_band_option_range(env):
     eng = env[0]
-    for bad in (0, -53, 5):
+    for bad in (0, -41, -53, 5):
         with pytest.raises(ValueError, match="band"):
             eng.set_sampler_band(bad)
     eng.set_sampler_band(DEFAULT)
@@ -157,3 +157,48 @@ def test_lora_set_async_tokens_are_settled_at_sync(env):
         eng.set_sampler_band(DEFAULT)
         _lib.check(L.th_dev_free(eng._h, hd))
         _lib.check(L.th_dev_free(eng._h, od))
+
+
+@pytest.mark.parametrize("sk_fused", [False, True])
+def test_no_sync_token_exposes_only_nan_or_exact_deltas(env, sk_fused):
+    """A token queued without a synchronisation whose inputs are flagged (wide band), its input
+    and output in ROCm torch tensors: a torch copy of its deltas ordered after it on the context
+    stream (a stream-ordered consumer, made before any settling call) holds NaN for every delta
+    of a flagged input's projections and the exact delta otherwise, never another value; after
+    th_ctx_sync the token's own output is exact. A later host-to-device copy into the token's
+    input (th_memcpy_h2d) settles the token first, so its redo reads the input it was queued
+    with."""
+    import torch
+
+    eng, ref, sk, pk, rsk, rpk = env
+    L = _lib.load()
+    rng = np.random.default_rng(67)
+    ls, _ = _lora(eng, rng)
+    H = np.ascontiguousarray(rng.normal(size=(2, 1024)) * 0.1)
+    H2 = np.ascontiguousarray(rng.normal(size=(2, 1024)) * 0.1)
+    seeds = np.ascontiguousarray([410, 411], np.uint64)
+    expect = np.concatenate(ls.deltas(pk, sk, H, seeds))
+    dev = torch.device("cuda:0")
+    ht = torch.from_numpy(H).to(dev)
+    out = torch.zeros(ls.n_deltas, dtype=torch.float64, device=dev)
+    torch.cuda.synchronize()
+    stream = C.c_void_p()
+    _lib.check(L.th_ctx_stream(eng._h, C.byref(stream)))
+    mode = zero_moai.LoraSet._mode(True, sk_fused)
+    before = eng.redrawn_inputs()
+    eng.set_sampler_band(WIDE)
+    try:
+        _lib.check(L.th_lora_deltas(eng._h, ls._h, eng._own(pk), eng._own(sk), ht.data_ptr(), 1, _lib.ptr(seeds),
+                                    mode, out.data_ptr(), 1, None))
+    finally:
+        eng.set_sampler_band(DEFAULT)
+    with torch.cuda.stream(torch.cuda.ExternalStream(stream.value)):
+        seen = out.clone()  # a consumer ordered after the token on its stream
+    _lib.check(L.th_memcpy_h2d(eng._h, C.c_void_p(ht.data_ptr()), _lib.ptr(H2), H2.nbytes))
+    assert eng.redrawn_inputs() - before == 2
+    eng.sync()
+    torch.cuda.synchronize()
+    seen_h, final = seen.cpu().numpy(), out.cpu().numpy()
+    assert np.array_equal(final, expect)
+    assert np.all(np.isnan(seen_h) | (seen_h == expect))
+    assert np.all(np.isnan(seen_h))  # both inputs flagged: every projection reads one of them
