@@ -499,7 +499,7 @@ def ntt_only(chain="default", n=N):
     if q is not None and n != N:
         raise SystemExit("--ntt-chain other than default is defined for N=16384 only")
     ctx = tensafe_he.CkksContext(n) if q is None else tensafe_he.CkksContext(n, moduli=q)
-    ntt = ntt_roofline(ctx, reps=5)
+    ntt = ntt_roofline(ctx, reps=60)
     copy_ms = copy_calibration(ctx, ntt["bytes_per_launch"] // 2)
     print(json.dumps({
         "metric": f"batched NTT achieved GB/s (64 polys x 4 limbs, N={n})",

@@ -85,8 +85,10 @@ int th_ctx_stream(th_ctx* ctx, void** stream);
  *     stream positions as the reference; draws whose rounding could depend on
  *     the math library are redrawn on the host (TH_OPT_SAMPLER_BAND);
  *   TH_SAMPLER_HOST - the host draws them exactly as the reference does.
- * TH_OPT_FORCE_SERIAL_SAMPLER: 1 makes the device sampler replay every
- *   stream serially (the path taken after a range_u32 rejection); testing only.
+ * TH_OPT_FORCE_SERIAL_SAMPLER: 1 makes the device samplers replay every
+ *   stream serially (the path taken after a range_u32 or range_u64
+ *   rejection), encrypt_pk's and the key and secret-key-encryption draws
+ *   alike; testing only.
  * TH_OPT_SAMPLER_BAND: v in [-40, -1], default -36: the device sampler flags
  *   every Gaussian draw whose z * 3.19 lies within 2^v of a rounding boundary
  *   k + 1/2 (where the device's log/cos could round differently from glibc's;

@@ -97,4 +97,39 @@ struct SampleJob {
 hipError_t launch_sample_pk(const SampleJob* jobs, uint32_t njobs, uint32_t n, int force_serial, hipStream_t s,
                             const uint64_t* seeds, bool flagged, bool fix_later, BandArgs band);
 
+// Key and secret-key-encryption randomness drawn on the device from the
+// reference's ChaCha20 stream (rng.rs:31-157, sampling.rs:17-64). A job is
+// one stretch of a stream: kind KEY_TERNARY is keygen's N x range_u32(3)
+// (ciphertext.rs:86-97), written as the signed values -1, 0, 1 it stands for;
+// kind KEY_UNIFORM_GAUSS is a = range_u64(q_l) for N coefficients of every
+// limb l = 0..L-1, then N rounded Gaussians e (keygen_public,
+// ciphertext.rs:119-127, and the secret-key encrypt, :183-196). Job j's draws
+// start at word word0 of the stream of its seed and are drawn in parallel as
+// if none of its words were rejected (launch_key_draws): *reject receives the
+// lowest index of a job that held a rejected word (range_u32: 0; range_u64:
+// r < 2^64 mod q_l), for which launch_key_replay draws that job serially in
+// the reference's order and writes the word where its draws ended to *end.
+// Gaussian draws near a rounding boundary raise their job's band flag
+// (BandArgs), for a redraw with glibc.
+enum : uint32_t { KEY_TERNARY = 0, KEY_UNIFORM_GAUSS = 1 };
+struct KeyDrawJob {
+  uint64_t seed;
+  uint64_t word0;
+  uint32_t kind;
+  uint32_t pad_;
+  int64_t* s;   // KEY_TERNARY: N values
+  uint64_t* a;  // KEY_UNIFORM_GAUSS: L x N residues, limb-major
+  int64_t* e;   // KEY_UNIFORM_GAUSS: N values
+};
+// Stream words a job of `kind` takes when none is rejected.
+__host__ __device__ inline uint64_t key_draw_words(uint32_t kind, uint32_t n, uint32_t L) {
+  return kind == KEY_TERNARY ? n : (uint64_t)(2 * L + 4) * n;
+}
+// reject: a device word that must hold 0xFFFFFFFF before the launch.
+hipError_t launch_key_draws(const KeyDrawJob* jobs, uint32_t njobs, uint32_t n, uint32_t L, const BarrettConst* bc,
+                            uint32_t* reject, BandArgs band, hipStream_t s);
+// Serial draws of one job (device job descriptor); band: the job's own flags.
+hipError_t launch_key_replay(const KeyDrawJob* job, uint32_t n, uint32_t L, const BarrettConst* bc, uint64_t* end,
+                             BandArgs band, hipStream_t s);
+
 }  // namespace th

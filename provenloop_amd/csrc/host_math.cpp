@@ -104,7 +104,7 @@ ChaChaStream::ChaChaStream(uint64_t seed) {
   next_block();
 }
 
-ChaChaStream ChaChaStream::from_os_entropy() {
+uint64_t os_entropy_seed() {
   uint64_t seed = 0;
   FILE* f = fopen("/dev/urandom", "rb");
   bool ok = false;
@@ -113,8 +113,10 @@ ChaChaStream ChaChaStream::from_os_entropy() {
     fclose(f);
   }
   if (!ok) seed = (uint64_t)(uintptr_t)&seed ^ 0xdeadbeefcafebabeULL;
-  return ChaChaStream(seed);
+  return seed;
 }
+
+ChaChaStream ChaChaStream::from_os_entropy() { return ChaChaStream(os_entropy_seed()); }
 
 void ChaChaStream::next_block() {
   const uint32_t in[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,

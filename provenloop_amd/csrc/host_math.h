@@ -24,6 +24,10 @@ uint64_t primitive_2n_root(uint32_t n, uint64_t q);
 
 // Deterministic ChaCha20 stream with the reference's seed expansion and
 // draw helpers (tensafe-he-core/src/rng.rs:31-157).
+// A seed from the OS (/dev/urandom): TenSafeRng::from_entropy's seed
+// (rng.rs:73-76, :210-221), for streams drawn on the device.
+uint64_t os_entropy_seed();
+
 class ChaChaStream {
  public:
   explicit ChaChaStream(uint64_t seed);

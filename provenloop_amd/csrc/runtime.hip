@@ -224,6 +224,9 @@ struct th_ctx {
   // the calls that sample.
   uint32_t* bflag_gen = nullptr;
   uint32_t band_gen = 0;
+  // launch_key_draws' reject word and launch_key_replay's end word (device)
+  uint32_t* key_reject = nullptr;
+  uint64_t* key_end = nullptr;
   std::vector<AsyncToken> pending;
   uint64_t redrawn_inputs = 0;  // inputs whose randomness was drawn again on the host (th_ctx_stats)
   std::unordered_set<void*> user_allocs;  // th_dev_alloc buffers not yet freed
@@ -735,7 +738,7 @@ void destroy_ctx(th_ctx* c) {
   c->pool.release_all();
   c->ring.destroy();
   void* bufs[] = {c->d_lc, c->d_bc, c->d_q, c->d_rc, c->d_dc, c->d_twist_re, c->d_twist_im,
-                  c->d_stage_re, c->d_stage_im, c->d_tables, c->bflag_gen};
+                  c->d_stage_re, c->d_stage_im, c->d_tables, c->bflag_gen, c->key_end};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   for (auto& kv : c->seg_w) (void)hipFree(kv.second);
@@ -754,11 +757,68 @@ void pad_input(const th_ctx* c, const double* z, size_t n, double* out) {
   if (m < S) memset(out + m, 0, (S - m) * 8);
 }
 
-// Upload signed coefficients and reduce them into L limb-polys at dst.
-void upload_signed(OpScope& sc, const std::vector<int64_t>& x, uint64_t* dst, uint32_t limbs) {
+
+void download(th_ctx* c, void* dst, const void* src_dev, size_t bytes);
+
+// The draws of device_key_draws' KEY_UNIFORM_GAUSS jobs made on the host with
+// glibc, for calls whose device draws had a Gaussian in the sampler's band:
+// `count` stretches of the stream of `seed`, input after input (a for every
+// limb, then e; ciphertext.rs:119-127, :183-196), uploaded to a[i] (L x N)
+// and e + i N.
+void host_key_draws(OpScope& sc, uint64_t seed, size_t count, uint64_t* const* a, int64_t* e) {
   th_ctx* c = sc.c;
-  const int64_t* d = sc.up(x);
-  HIPCHK(launch_signed_to_rns(d, dst, c->d_bc, c->N, limbs, c->stream));
+  const uint32_t N = c->N, L = c->L;
+  ChaChaStream s(seed);
+  std::vector<uint64_t> av((size_t)L * N);
+  std::vector<int64_t> ev((size_t)count * N);
+  for (size_t i = 0; i < count; ++i) {
+    for (uint32_t l = 0; l < L; ++l)
+      for (uint32_t k = 0; k < N; ++k) av[(size_t)l * N + k] = s.below_u64(c->q[l]);
+    draw_gaussian(s, N, ev.data() + i * N);
+    HIPCHK(hipMemcpyAsync(a[i], sc.up(av), av.size() * 8, hipMemcpyDeviceToDevice, c->stream));
+  }
+  HIPCHK(hipMemcpyAsync(e, sc.up(ev), ev.size() * 8, hipMemcpyDeviceToDevice, c->stream));
+}
+
+// Key and secret-key-encryption draws (launch_key_draws) for `jobs`,
+// consecutive stretches of one stream: job i starts where job i - 1's draws
+// end. Every job is drawn in parallel as if no word were rejected; from the
+// first job that held a rejected word, that job is drawn serially
+// (launch_key_replay) and the jobs after it are drawn again in parallel from
+// where it ended, until no rejection is left. Waits for the stream. Returns
+// whether a Gaussian draw landed in the sampler's band, in which case the
+// caller draws the randomness again on the host with glibc.
+bool device_key_draws(th_ctx* c, std::vector<KeyDrawJob> jobs) {
+  const uint32_t N = c->N, L = c->L, nj = (uint32_t)jobs.size();
+  if (!nj) return false;
+  const uint32_t off = take_flags(c, nj);
+  const BandArgs band{c->bflag_dev + off, c->band};
+  uint64_t word = jobs[0].word0;
+  for (uint32_t j = 0; j < nj;) {
+    for (uint32_t i = j; i < nj; ++i) {
+      jobs[i].word0 = word;
+      word += key_draw_words(jobs[i].kind, N, L);
+    }
+    OpScope sc(c);
+    const KeyDrawJob* dj = (const KeyDrawJob*)sc.upload(jobs.data() + j, (nj - j) * sizeof(KeyDrawJob));
+    const uint32_t none = 0xFFFFFFFFu;
+    void* h = c->ring.reserve(4, c->stream);
+    memcpy(h, &none, 4);
+    HIPCHK(hipMemcpyAsync(c->key_reject, h, 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(launch_key_draws(dj, nj - j, N, L, c->d_bc, c->key_reject, band_from(band, j), c->stream));
+    uint32_t r = 0;
+    download(c, &r, c->key_reject, 4);
+    if (c->force_serial) r = 0;  // TH_OPT_FORCE_SERIAL_SAMPLER: every job drawn serially (testing)
+    if (r >= nj - j) break;
+    // job j + r and the ones after it move: their flags from this pass do not count
+    memset(c->bflag_host + off + j + r, 0, nj - j - r);
+    HIPCHK(launch_key_replay(dj + r, N, L, c->d_bc, c->key_end, band_from(band, j + r), c->stream));
+    download(c, &word, c->key_end, 8);
+    j += r + 1;
+  }
+  const bool flagged = any_flag(c, off, nj);
+  release_flags(c, off);
+  return flagged;
 }
 
 // GPU encode of `count` padded inputs (device, count x N/2) into dst + i*dst_stride:
@@ -1264,6 +1324,8 @@ int th_ctx_create(uint32_t N, const uint64_t* moduli, uint32_t L, uint32_t scale
       HIPCHK(hipHostGetDevicePointer((void**)&c->bflag_dev, c->bflag_host, 0));
       HIPCHK(hipMalloc((void**)&c->bflag_gen, (size_t)c->bflag_cap * 4));
       HIPCHK(hipMemset(c->bflag_gen, 0, (size_t)c->bflag_cap * 4));
+      HIPCHK(hipMalloc((void**)&c->key_end, 16));  // the end word, then the reject word
+      c->key_reject = reinterpret_cast<uint32_t*>(c->key_end + 1);
     } catch (...) {
       destroy_ctx(c);
       throw;
@@ -1330,16 +1392,15 @@ int th_keygen(th_ctx* ctx, uint64_t seed, int has_seed, th_sk** out) {
     TH_LOCK(ctx);
     need(out != nullptr, "null output");
     const uint32_t N = ctx->N, L = ctx->L;
-    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
-    std::vector<uint8_t> t(N);
-    draw_ternary(s, N, t.data());  // ciphertext.rs:86
-    std::vector<int64_t> v(N);
-    for (uint32_t i = 0; i < N; ++i) v[i] = t[i] == 0 ? -1 : (t[i] == 1 ? 0 : 1);  // ciphertext.rs:91-96
+    const uint64_t sd = has_seed ? seed : os_entropy_seed();  // rng.rs:73-76
     th_sk* sk = adopt(new th_sk{ctx, nullptr});
     try {
       sk->d = (uint64_t*)ctx->pool.get(L * poly_bytes(ctx));
       OpScope sc(ctx);
-      upload_signed(sc, v, sk->d, L);
+      int64_t* v = (int64_t*)sc.dev((size_t)N * 8);
+      // s: N x range_u32(3) as -1, 0, 1 (ciphertext.rs:86-97), on every limb, then NTT
+      device_key_draws(ctx, {KeyDrawJob{sd, 0, KEY_TERNARY, 0, v, nullptr, nullptr}});
+      HIPCHK(launch_signed_to_rns(v, sk->d, ctx->d_bc, N, L, ctx->stream));
       ntt_strided(ctx, false, sk->d, sk->d, L, L);
     } catch (...) {
       drop(sk);
@@ -1354,23 +1415,22 @@ int th_keygen_public(th_ctx* ctx, const th_sk* sk, uint64_t seed, int has_seed, 
     TH_LOCK(ctx);
     need(out != nullptr && sk != nullptr && sk->ctx == ctx, "bad secret key");
     const uint32_t N = ctx->N, L = ctx->L;
-    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
-    // ciphertext.rs:119-127: a for every limb, then e
-    std::vector<uint64_t> a((size_t)L * N);
-    for (uint32_t l = 0; l < L; ++l)
-      for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
-    std::vector<int64_t> e(N);
-    draw_gaussian(s, N, e.data());
+    const uint64_t sd = has_seed ? seed : os_entropy_seed();
     th_pk* pk = adopt(new th_pk{ctx, nullptr});
     try {
       pk->d = (uint64_t*)ctx->pool.get(2 * L * poly_bytes(ctx));
       uint64_t* b = pk->d;
       uint64_t* ad = pk->d + (size_t)L * N;
       OpScope sc(ctx);
+      int64_t* e = (int64_t*)sc.dev((size_t)N * 8);
       uint64_t* etmp = (uint64_t*)sc.dev(L * poly_bytes(ctx));
-      const uint64_t* a_up = sc.up(a);
-      HIPCHK(hipMemcpyAsync(ad, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
-      upload_signed(sc, e, etmp, L);
+      // ciphertext.rs:119-127: a for every limb, then e, drawn on the device;
+      // a Gaussian draw in the sampler's band: all of it again with glibc
+      if (device_key_draws(ctx, {KeyDrawJob{sd, 0, KEY_UNIFORM_GAUSS, 0, nullptr, ad, e}})) {
+        host_key_draws(sc, sd, 1, &ad, e);
+        ctx->redrawn_inputs += 1;
+      }
+      HIPCHK(launch_signed_to_rns(e, etmp, ctx->d_bc, N, L, ctx->stream));
       ntt_strided(ctx, false, ad, ad, L, L);
       ntt_strided(ctx, false, etmp, etmp, L, L);
       HIPCHK(launch_sub_product(etmp, ad, sk->d, b, ctx->d_bc, N, L, ctx->stream));  // b = e - a*s
@@ -1419,32 +1479,43 @@ int th_pk_download(th_ctx* ctx, const th_pk* pk, uint64_t* b, uint64_t* a) {
 }  // extern "C"
 
 namespace {
-// Secret-key encryption of one padded input with randomness from `s`
-// (ciphertext.rs:167-229: encode, a for every limb, then e).
-th_ct* encrypt_sk_one(th_ctx* ctx, const th_sk* sk, const std::vector<double>& pad, ChaChaStream& s) {
+// Secret-key encryption (ciphertext.rs:167-229) of `count` padded inputs
+// (host, count x N/2) drawing from ONE stream seeded with `seed`, input after
+// input (batch_encrypt's shared RNG, lib.rs:230-258): per input, a on every
+// limb then e (on the device; all of it again with glibc on the host when a
+// Gaussian lands in the sampler's band); encode m + e; c1 = NTT(a),
+// c0 = NTT(m + e) - c1 s.
+std::vector<th_ct*> encrypt_sk_many(th_ctx* ctx, const th_sk* sk, const std::vector<double>& pads, size_t count,
+                                    uint64_t seed) {
   const uint32_t N = ctx->N, L = ctx->L;
-  std::vector<uint64_t> a((size_t)L * N);
-  for (uint32_t l = 0; l < L; ++l)
-    for (uint32_t i = 0; i < N; ++i) a[(size_t)l * N + i] = s.below_u64(ctx->q[l]);
-  std::vector<int64_t> e(N);
-  draw_gaussian(s, N, e.data());
-  th_ct* ct = new_ct(ctx, L, kScale);
-  uint64_t* c0 = ct->d;
-  uint64_t* c1 = ct->d + (size_t)L * N;
+  std::vector<th_ct*> made;
   try {
+    for (size_t i = 0; i < count; ++i) made.push_back(new_ct(ctx, L, kScale));
+    if (!count) return made;
     OpScope sc(ctx);
-    uint64_t* me = (uint64_t*)sc.dev(L * poly_bytes(ctx));
-    queue_encode(sc, sc.up(pad), 1, nullptr, sc.up(e), nullptr, me, 0);  // M = m + e
-    const uint64_t* a_up = sc.up(a);
-    HIPCHK(hipMemcpyAsync(c1, a_up, a.size() * 8, hipMemcpyDeviceToDevice, ctx->stream));
-    ntt_strided(ctx, false, me, me, L, L);
-    ntt_strided(ctx, false, c1, c1, L, L);
-    HIPCHK(launch_sub_product(me, c1, sk->d, c0, ctx->d_bc, N, L, ctx->stream));  // c0 = (m + e) - a*s
+    int64_t* e = (int64_t*)sc.dev(count * N * 8);
+    uint64_t* me = (uint64_t*)sc.dev(count * L * poly_bytes(ctx));
+    std::vector<KeyDrawJob> jobs(count);
+    std::vector<uint64_t*> a(count);
+    for (size_t i = 0; i < count; ++i) {
+      a[i] = made[i]->d + (size_t)L * N;  // c1 = a, transformed below
+      jobs[i] = KeyDrawJob{seed, 0, KEY_UNIFORM_GAUSS, 0, nullptr, a[i], e + i * N};
+    }
+    if (device_key_draws(ctx, jobs)) {
+      host_key_draws(sc, seed, count, a.data(), e);
+      ctx->redrawn_inputs += count;
+    }
+    queue_encode(sc, sc.up(pads), count, nullptr, e, nullptr, me, (size_t)L * N);  // M = m + e
+    for (size_t i = 0; i < count; ++i) {
+      uint64_t* m = me + i * L * N;
+      ntt_strided(ctx, false, m, m, L, L);
+      ntt_strided(ctx, false, a[i], a[i], L, L);
+      HIPCHK(launch_sub_product(m, a[i], sk->d, made[i]->d, ctx->d_bc, N, L, ctx->stream));  // c0 = (m + e) - a*s
+    }
   } catch (...) {
-    drop(ct);
-    throw;
+    drop_all_rethrow(made);
   }
-  return ct;
+  return made;
 }
 }  // namespace
 
@@ -1457,8 +1528,7 @@ int th_encrypt(th_ctx* ctx, const th_sk* sk, const double* z, size_t n, uint64_t
     need(z != nullptr || n == 0, "null input");
     std::vector<double> pad(ctx->N / 2);
     pad_input(ctx, z, n, pad.data());
-    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();
-    *out = encrypt_sk_one(ctx, sk, pad, s);
+    *out = encrypt_sk_many(ctx, sk, pad, 1, has_seed ? seed : os_entropy_seed())[0];
   });
 }
 
@@ -1467,17 +1537,11 @@ int th_encrypt_batch(th_ctx* ctx, const th_sk* sk, const double* z, const uint64
   return guarded([&] {
     TH_LOCK(ctx);
     need(outs && sk && sk->ctx == ctx && (count == 0 || (z && lens)), "bad argument");
-    ChaChaStream s = has_seed ? ChaChaStream(seed) : ChaChaStream::from_os_entropy();  // lib.rs:238-241
-    std::vector<th_ct*> made;
-    try {
-      for (size_t i = 0; i < count; ++i) {
-        std::vector<double> pad(ctx->N / 2);
-        pad_input(ctx, z + i * stride, (size_t)lens[i], pad.data());
-        made.push_back(encrypt_sk_one(ctx, sk, pad, s));
-      }
-    } catch (...) {
-      drop_all_rethrow(made);
-    }
+    const size_t S = ctx->N / 2;
+    std::vector<double> pads(count * S);
+    for (size_t i = 0; i < count; ++i) pad_input(ctx, z + i * stride, (size_t)lens[i], pads.data() + i * S);
+    const std::vector<th_ct*> made =
+        encrypt_sk_many(ctx, sk, pads, count, has_seed ? seed : os_entropy_seed());  // lib.rs:238-241
     for (size_t i = 0; i < count; ++i) outs[i] = made[i];
   });
 }

@@ -114,7 +114,8 @@ static __device__ __forceinline__ uint64_t job_seed(const SampleJob& jb, const S
 // Serial replay of the reference's consumption order for one stream.
 struct SerialStream {
   uint32_t lo, hi, counter, pos, w[16];
-  __device__ explicit SerialStream(uint64_t seed) : lo((uint32_t)seed), hi((uint32_t)(seed >> 32)), counter(0), pos(16) {}
+  __device__ explicit SerialStream(uint64_t seed, uint32_t block = 0)
+      : lo((uint32_t)seed), hi((uint32_t)(seed >> 32)), counter(block), pos(16) {}
   __device__ uint32_t next() {
     if (pos == 16) {
       chacha20(lo, hi, counter, w);
@@ -153,7 +154,7 @@ static __device__ void serial_replay(const SampleJob& jb, uint64_t seed, uint32_
 // The end of a flagged sampler launch for job j: replay the stream serially
 // if a u word was rejected (or force_serial), then clear the flag. Run by one
 // thread, in a launch ordered after the block kernel.
-static __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial,
+inline __device__ void sample_fix_job(const SampleJob& jb, uint64_t seed, uint32_t n, int force_serial,
                                       const FlagOut& flag, double band) {
   if (*jb.reject || force_serial) serial_replay(jb, seed, n, flag, band);
   *jb.reject = 0;
