@@ -765,6 +765,64 @@ def single_delta_workload(ctx, sk, pk, cpu, reps=100, warm=10):
     }
 
 
+def drop_in_workload(ctx, sk, A, B, hidden, steps=3, warm=1):
+    """The reference's own per-token call sequence through the drop-in Python
+    module (provenloop_amd.adapter / tensafe_he), one call at a time as the
+    engine makes them (inference_engine.py:1244-1392): per projection of each
+    of the 28 layers, encrypt_vector of the replicated hidden state (secret-key
+    encrypt, :166-176, :1266-1272), then per packed LoRA-A batch
+    `ct_rep * packed_pt` (ct x pt with the plaintext encoded on the fly,
+    lib.rs:336-356) and decrypt_to_gpu (:1311-1315), the batches' slots
+    stacked on the GPU and copied to the host once, the segment sums and
+    B @ intermediate on the host (:1379-1392). ms per token and deltas/s, and
+    the deltas against B (A h) in plaintext."""
+    import torch
+
+    from provenloop_amd import zero_moai
+    from provenloop_amd.adapter import TenSafeHEAdapter
+
+    adp = TenSafeHEAdapter(ctx, sk)
+    S, cols = N // 2, (N // 2) // D
+    packed = {k: zero_moai.pack_rows(np.asarray(A[k], np.float64), S) for k in A}  # the engine's _packed_pts
+
+    def token(hs):
+        out = {}
+        for l in range(LAYERS):
+            for p in "qv":
+                ct_rep = adp.encrypt_vector(zero_moai.replicate(hs[l], S, D))
+                decs = [adp.decrypt_to_gpu(ct_rep * pt) for pt in packed[(l, p)]]
+                all_dec = torch.stack(decs).cpu().numpy()
+                inter = np.zeros(RANK)
+                for b in range(len(decs)):
+                    for i, r in enumerate(range(b * cols, min((b + 1) * cols, RANK))):
+                        inter[r] = np.sum(all_dec[b, i * D:(i + 1) * D])
+                out[(l, p)] = np.asarray(B[(l, p)], np.float64) @ inter
+        return out
+
+    for w in range(warm):
+        token(hidden[w % len(hidden)])
+    t0 = time.perf_counter()
+    for t in range(steps):
+        got = token(hidden[t % len(hidden)])
+    elapsed = time.perf_counter() - t0
+    hs = hidden[(steps - 1) % len(hidden)]
+    rel = []
+    for l in (0, LAYERS - 1):
+        for p in "qv":
+            e = np.asarray(B[(l, p)], np.float64) @ (np.asarray(A[(l, p)], np.float64) @ hs[l])
+            rel.append(float(np.linalg.norm(got[(l, p)] - e) / np.linalg.norm(e)))
+    return {
+        "value": round(LAYERS * 2 * steps / elapsed, 3), "unit": "deltas/s", "ms_per_step": round(elapsed / steps * 1e3, 3),
+        "steps": steps, "warmup": warm,
+        "workload": "the reference's per-token call sequence through the drop-in module, one call at a time: per "
+                    "projection of 28 layers, adapter.encrypt_vector (secret key, unseeded), 4 x ct_rep * packed_pt "
+                    "(plaintext encoded per call) and decrypt_to_gpu, one stack and host copy, segment sums and "
+                    "B @ intermediate on the host (inference_engine.py:1244-1392); 56 encryptions, 224 products "
+                    "and 224 decryptions with their host synchronisations per token",
+        "parity": {"delta_rel_err_vs_plaintext_max_layers_0_27": max(rel)},
+    }
+
+
 def run_single(args):
     """Only the single-delta figure, for a kernel trace of its
     launches: the same calls as the reported line's single_delta."""
@@ -805,10 +863,11 @@ def main():
                          "60-bit (integer butterfly path) or four 40-bit (FP64 butterfly path) primes")
     ap.add_argument("--ntt-n", type=int, choices=(16384, 32768), default=N,
                     help="ring degree of the --ntt-only launches (reference chain for that degree)")
-    ap.add_argument("--workload", choices=("token", "moe", "saturation", "single"), default="token",
+    ap.add_argument("--workload", choices=("token", "moe", "saturation", "single", "dropin"), default="token",
                     help="token: the per-token Qwen2.5-1.5B pass (the reported line); moe: its CryptoMOE "
                          "variant with a per-token gate; saturation: 32 sessions at Qwen2.5-7B shape on "
-                         "N=32768 with 8 limbs; single: one encrypted delta's latency")
+                         "N=32768 with 8 limbs; single: one encrypted delta's latency; dropin: the reference's "
+                         "per-token call sequence through the drop-in module")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 20 if args.workload == "saturation" else 100
@@ -829,6 +888,20 @@ def main():
         return
     if args.workload == "single":
         run_single(args)
+        return
+    if args.workload == "dropin":
+        from provenloop_amd import tensafe_he
+
+        A, B = make_workload()
+        ctx = tensafe_he.CkksContext(N)
+        sk = ctx.keygen(seed=11)
+        r = drop_in_workload(ctx, sk, A, B, [hidden_states(t) for t in range(args.steps)], steps=args.steps,
+                             warm=args.warmup)
+        print(json.dumps(dict({
+            "metric": "encrypted LoRA deltas/s through the drop-in module in the reference's call sequence",
+            "n_gpus": 1, "higher_is_better": True, "dtype": "u64", "data": "synthetic (seeded, as the token pass)",
+            "config": {"workload": r.pop("workload"), "N": N},
+        }, **r)), flush=True)
         return
 
     A, B = make_workload()
@@ -960,6 +1033,7 @@ def main():
     extra = {}
     if not args.no_extra:
         extra["single_delta"] = single_delta_workload(ctx, sk, pk, cpu)
+        extra["drop_in_sequence"] = drop_in_workload(ctx, sk, A, B, [hidden[t] for t in range(args.steps)])
         del lora
         extra["moe"] = moe_workload(steps=10, warmup=2)
         extra["saturation"] = saturation_workload(steps=3, warmup=1)
