@@ -760,8 +760,9 @@ __global__ __launch_bounds__(64) void rd_row_kernel(RescaleDecryptArgs a) {
 
 // Step 4. Workgroup w: column part w % PARTS of batch w / PARTS; writes
 // lane t's sums for segments c < cols at partials + (b cols + c) T + t,
-// T = 2^(LOGN-4).
-template <int LOGN>
+// T = 2^(LOGN-4). Without RESCALED (a plain decryption, launch_decrypt_sums_split)
+// the decrypted coefficient is the transform's output itself.
+template <int LOGN, bool RESCALED = true>
 __global__ __launch_bounds__(64) void rd_column_sums_kernel(RescaleDecryptArgs a, double* __restrict__ partials) {
   using S = Split<LOGN>;
   constexpr int MAXC = NTT_SEGSUM_FUSED_MAX_COLS;
@@ -771,7 +772,7 @@ __global__ __launch_bounds__(64) void rd_column_sums_kernel(RescaleDecryptArgs a
   const RescaleDecryptJob jb = a.jobs[b];
   const ColumnMap<LOGN> m(column_part<LOGN>(blockIdx.x % S::PARTS));
   const LimbConst& lc = a.lc[0];
-  const RescaleConst rc = *a.rc;
+  const RescaleConst rc = RESCALED ? *a.rc : RescaleConst{};
   const uint64_t q = lc.q, half = q >> 1;
   uint64_t mv[16];
   if (lc.fp64) {
@@ -789,14 +790,14 @@ __global__ __launch_bounds__(64) void rd_column_sums_kernel(RescaleDecryptArgs a
   }
   using D2 = double __attribute__((ext_vector_type(2)));
   const GPtr<D2> W = gld(reinterpret_cast<const D2*>(a.segw));
-  const GPtr<uint64_t> r0 = gld(jb.x);
+  const GPtr<uint64_t> r0 = gld(RESCALED ? jb.x : jb.y);
   double acc[MAXC];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) acc[c] = 0.0;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const uint32_t j = m.j1(k);
-    const uint64_t v0 = csub(shoup_lazy(submod(mv[k], r0[j], q), rc.inv, rc.inv_s, q), q);
+    const uint64_t v0 = RESCALED ? csub(shoup_lazy(submod(mv[k], r0[j], q), rc.inv, rc.inv_s, q), q) : mv[k];
     const double v = v0 > half ? -(double)(q - v0) : (double)v0;
     const D2 p = W[j];  // W_0[j], 2 cos(2 phi_j)
     double wp = p.x, wc = p.x;
@@ -852,6 +853,34 @@ static hipError_t launch_rd_split_t(const NttArgs& inv, const RescaleDecryptArgs
   hipLaunchKernelGGL((rd_column_sums_kernel<LOGN>), dim3(nb * S::PARTS), block, 0, s, a, partials);
   hipLaunchKernelGGL((rd_sums_final_kernel<LOGN>), dim3(nb * a.cols), block, 0, s, a, (const double*)partials);
   return hipGetLastError();
+}
+
+// A plain batched decryption with segment sums on the split kernels: the
+// inverse row pass of c0 + c1 s (row: NTT_LOAD_DOTM jobs on limb 0, one per
+// batch, dst = the batch's y), then steps 4 and 5 without the rescale.
+template <int LOGN>
+static hipError_t launch_dec_split_t(const NttArgs& row, const RescaleDecryptArgs& a, uint32_t nb, double* partials,
+                                     hipStream_t s) {
+  using S = Split<LOGN>;
+  const dim3 block(64);
+  hipLaunchKernelGGL((ntt_split_kernel<LOGN, true, false, NTT_LOAD_DOTM, NTT_STORE_NONE>), dim3(nb * S::PARTS), block,
+                     0, s, row);
+  hipLaunchKernelGGL((rd_column_sums_kernel<LOGN, false>), dim3(nb * S::PARTS), block, 0, s, a, partials);
+  hipLaunchKernelGGL((rd_sums_final_kernel<LOGN>), dim3(nb * a.cols), block, 0, s, a, (const double*)partials);
+  return hipGetLastError();
+}
+
+hipError_t launch_decrypt_sums_split(int logn, const NttArgs& row, const RescaleDecryptArgs& a, uint32_t nb,
+                                     double* partials, hipStream_t s) {
+  if (nb == 0) return hipSuccess;
+  if (!row.jobs || row.load != NTT_LOAD_DOTM || a.cols < 1 || a.cols > NTT_SEGSUM_FUSED_MAX_COLS)
+    return hipErrorInvalidValue;
+  switch (logn) {
+    case 13: return launch_dec_split_t<13>(row, a, nb, partials, s);
+    case 14: return launch_dec_split_t<14>(row, a, nb, partials, s);
+    case 15: return launch_dec_split_t<15>(row, a, nb, partials, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_rescale_decrypt_split(int logn, const NttArgs& inv, const RescaleDecryptArgs& a, uint32_t nb,

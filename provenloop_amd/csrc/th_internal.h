@@ -1,5 +1,6 @@
-// Host-side declarations shared between the runtime (runtime.cpp) and the
-// kernel translation units. Not part of the public C ABI.
+// Host-side declarations shared between the host runtime (runtime.h and its
+// translation units) and the kernel translation units. Not part of the public
+// C ABI.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <atomic>
@@ -184,6 +185,15 @@ hipError_t launch_rescale_decrypt(int logn, const RescaleDecryptArgs& a, uint32_
 // bit for bit at N = 16384.
 hipError_t launch_rescale_decrypt_split(int logn, const NttArgs& inv, const RescaleDecryptArgs& a, uint32_t nb,
                                         double* partials, hipStream_t s);
+// A plain batched decryption with segment sums on the split kernels (N =
+// 8192 .. 32768) for nb batches: row = the nb inverse jobs of c0 + c1 s on
+// limb 0 (src = c0, aux = c1, load NTT_LOAD_DOTM with row.key the secret key
+// in Montgomery form, dst = the batch's work area, which a.jobs[b].y names
+// too); a.jobs[b].seg and .scale as for the rescale-decrypt; partials: nb x
+// cols x N/16 doubles. At N = 16384 the sums equal, bit for bit, those of the
+// whole-polynomial decrypt's segment-sum epilogue (NTT_STORE_SEGSUM).
+hipError_t launch_decrypt_sums_split(int logn, const NttArgs& row, const RescaleDecryptArgs& a, uint32_t nb,
+                                     double* partials, hipStream_t s);
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;

@@ -3,7 +3,7 @@
 mont_mul (provenloop_amd/csrc/th_device.h) returns a b 2^-64 mod q in [0, 2q)
 for any 64-bit a and b < q from T = a b and k = T_lo (-q^{-1}) mod 2^64 as
 t_hi + hi64(k q) + (T_lo != 0); -q^{-1} mod 2^64 comes from Newton's
-iteration (runtime.hip, six steps from 1) and operands are put into
+iteration (runtime_common.hip, six steps from 1) and operands are put into
 Montgomery form as w (2^64 mod q) mod q (k_to_montgomery). This model
 repeats the 64-bit steps with Python integers and checks, for every limb
 prime the library uses, the inverse, the bound, and that a product with a
