@@ -9,6 +9,7 @@
 
 #include <vector>
 
+#include "band.h"
 #include "host_math.h"
 
 using namespace th;
@@ -111,6 +112,24 @@ int main() {
     segment_weight_pairs(n, d, p.data());
     put_f64("segw_1024_100_5", w.data(), w.size());
     put_f64("segp_1024_100", p.data(), p.size());
+  }
+  {
+    // the sampler's band test on values next to rounding boundaries, far from
+    // them, at the exactness limit 2^52 and not finite (each value, then the
+    // flags for bands 2^-36 and 2^-40)
+    const double h = 0x1p-36;
+    const double t[] = {0.5, 2.5 + 0x1p-40, 2.5 - 0x1p-40, 2.5 + 0x1p-37, 2.5 - 0x1p-37, 2.5 + h, 2.5 - h,
+                        2.5 + 0x1p-35, -3.5 + 0x1p-38, -3.5 - 0x1p-34, 7.25, -0.75, 0.0, 27.5 + 0x1p-45,
+                        0x1p51 + 0.5, 0x1p52, -0x1p52, 1.0 / 0.0, -1.0 / 0.0, 0.0 / 0.0};
+    const size_t n = sizeof(t) / sizeof(t[0]);
+    std::vector<uint64_t> f36, f40;
+    for (double v : t) {
+      f36.push_back(near_rounding_boundary(v, 0x1p-36) ? 1 : 0);
+      f40.push_back(near_rounding_boundary(v, 0x1p-40) ? 1 : 0);
+    }
+    put_f64("band_t", t, n);
+    put_u64("band_flag_36", f36.data(), n);
+    put_u64("band_flag_40", f40.data(), n);
   }
   return 0;
 }

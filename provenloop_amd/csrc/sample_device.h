@@ -3,6 +3,7 @@
 // and by the encoder's kernels, which can draw a token's randomness beside the
 // encoding and finish the sampler's rejection handling.
 #pragma once
+#include "band.h"
 #include "encode_sample.h"
 
 namespace th {
@@ -37,18 +38,6 @@ static __device__ __forceinline__ uint8_t ternary_value(uint32_t w) {
 static __device__ __forceinline__ double unit_open(uint32_t w0, uint32_t w1) {
   const uint64_t v = (uint64_t)w0 | ((uint64_t)w1 << 32);  // next_u64: lo word first (rng.rs:99-103)
   return ((double)(v >> 11) + 0.5) / 9007199254740992.0;     // rng.rs:139-144
-}
-
-// Where a sample's rounding could depend on the math library: t = z * 3.19
-// within `band` of a rounding boundary k + 1/2, or not finite. The device's
-// log/cos differ from glibc's (which the reference calls through Rust std) by
-// a few ulps, so |t_device - t_glibc| stays below about 2^-45 (|z| < 8.7,
-// |t| < 28); with the default band of 2^-36 every sample whose rounded value
-// could differ from glibc's is flagged, and the host redraws it with glibc.
-// t - floor(t) and the difference from 1/2 are exact for |t| < 2^52.
-static __device__ __forceinline__ bool near_rounding_boundary(double t, double band) {
-  if (!(fabs(t) < 0x1p52)) return true;
-  return fabs((t - floor(t)) - 0.5) < band;
 }
 
 static __device__ __forceinline__ int64_t gaussian_rounded(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,

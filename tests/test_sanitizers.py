@@ -99,3 +99,25 @@ def test_oracle_tests_under_sanitizers():
     tail = (r.stdout + r.stderr)[-4000:]
     assert r.returncode == 0, tail
     assert "runtime error" not in r.stderr and "ERROR: AddressSanitizer" not in r.stderr, tail
+
+
+def test_sampler_band_predicate(host_math_out):
+    """The device sampler's boundary-band test (band.h, constexpr, the same definition the GPU
+    runs) against exact rational arithmetic: flagged iff t is not finite, |t| >= 2^52, or t lies
+    strictly within the band of k + 1/2."""
+    from fractions import Fraction
+
+    o = host_math_out
+    t = _f64(o["band_t"])
+    for key, band in (("band_flag_36", Fraction(1, 2 ** 36)), ("band_flag_40", Fraction(1, 2 ** 40))):
+        got = [int(v) for v in o[key]]
+        exp = []
+        for v in t:
+            if not np.isfinite(v) or abs(v) >= 2.0 ** 52:
+                exp.append(1)
+                continue
+            f = Fraction(float(v))
+            frac = f - (f.numerator // f.denominator)
+            exp.append(int(abs(frac - Fraction(1, 2)) < band))
+        assert got == exp, (key, got, exp)
+    assert sum(int(v) for v in o["band_flag_36"]) >= 8  # the test values do reach both sides
