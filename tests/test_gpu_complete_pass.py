@@ -111,6 +111,30 @@ def test_complete_token_full_shape(env):
     _check_token(eng, ref, rpk, ls, H, seeds, proj, True, layers=(0, 27))
 
 
+@pytest.mark.parametrize("n,chain,d", [(8192, None, 1536), (32768, "L8", 3584)])
+def test_complete_token_other_rings(n, chain, d):
+    """The complete token at N=8192 (the reference chain, 3 limbs) and at N=32768 on the 8-limb
+    chain of the Qwen2.5-7B saturation shape (a rescale forms 7 limbs of each product): one layer
+    x {q, v}, every input ciphertext and rescaled product equal to the oracle's, sums equal to
+    the sk-fused shortcut's."""
+    from provenloop_amd.params import CHAIN_N32768_L8
+
+    moduli = CHAIN_N32768_L8 if chain == "L8" else None
+    eng = tensafe_he.CkksContext(n) if moduli is None else tensafe_he.CkksContext(n, moduli=moduli)
+    ref = orc.Context(n, moduli=moduli)
+    sk, rsk = eng.keygen(seed=71), ref.keygen(71)
+    pk, rpk = eng.keygen_public(sk, seed=72), ref.keygen_public(rsk, 72)
+    rng = np.random.default_rng(33)
+    H = rng.normal(size=(1, d)) * 0.1
+    proj = [(0, rng.normal(size=(16, d)) * 0.02, rng.normal(size=(o, 16)) * 0.02) for o in (d, 128)]
+    ls = zero_moai.LoraSet(eng, 1, proj)
+    seeds = [3301]
+    _, sums_f = ls.deltas(pk, sk, H, seeds, with_intermediates=True, sk_fused=True)
+    _, sums = ls.deltas(pk, sk, H, seeds, with_intermediates=True)
+    assert np.array_equal(sums, sums_f)
+    _check_token(eng, ref, rpk, ls, H, seeds, proj, True, layers=(0,))
+
+
 def test_complete_moe_products_are_ct_add_of_expert_products(env):
     """CryptoMOE set: each batch's rescaled product equals the oracle's k expert products
     (ct_pt_mul with g_x A_x rows), folded with ct_add and rescaled, bit for bit
