@@ -534,7 +534,7 @@ def moe_gates(t, n_proj, k):
 
 
 def moe_workload(steps, warmup):
-    """CryptoMOE variant of the per-token pass: 3 rank-16
+    """CryptoMOE variant of the per-token pass (Qwen2.5-1.5B shape): 3 rank-16
     expert adapters per projection and a softmax gate that changes every
     token. Per token: th_lora_set_gates (the k gate-scaled plaintexts of every
     batch encoded, transformed and folded, and sum_x g_x B_x, on the device),
@@ -629,7 +629,7 @@ def run_moe(args):
 
 
 def saturation_workload(steps, warmup, parity_checks=((0, 4 * 27), (0, 4 * 27 + 3), (31, 4 * 27), (31, 4 * 27 + 3))):
-    """Saturation run at Qwen2.5-7B shape (BASELINE config 5): 32 sessions (own
+    """Saturation run at Qwen2.5-7B shape: 32 sessions (own
     keys), hidden 3584, 28 layers x {q,k,v,o}, rank 32, N=32768 on the 8-limb
     chain; one step = one token of every session, queued back to back with
     one synchronisation. Parity: (session, projection) pairs of the last step
@@ -713,7 +713,7 @@ def run_saturation(args):
 
 
 def single_delta_workload(ctx, sk, pk, cpu, reps=100, warm=10):
-    """One encrypted LoRA delta: encrypt_pk of the replicated
+    """One encrypted LoRA delta at N=16384: encrypt_pk of the replicated
     hidden state, 4 column-packed ct x pt products with cached plaintexts,
     rescale, decrypt with segment sums: 16 floats, host input and output, one
     synchronisation per delta. Latency = median over `reps` calls; parity and
@@ -820,7 +820,7 @@ def drop_in_workload(ctx, sk, A, B, hidden, steps=3, warm=1):
 
 
 def run_single(args):
-    """Only the single-delta figure, for a kernel trace of its
+    """Only the single-delta figure (one encrypted delta), for a kernel trace of its
     launches: the same calls as the reported line's single_delta."""
     from oracle import oracle as orc
     from provenloop_amd import tensafe_he

@@ -277,7 +277,8 @@ int th_lora_free(th_lora* set);
 int th_lora_info(const th_lora* set, uint64_t* n_deltas, uint32_t* n_batches, uint32_t* cols);
 /* th_lora_deltas mode bits.
  * TH_LORA_RESCALE: rescale each product before decrypting it
- *   (ciphertext.rs:476-535), as the LoRA pass at BASELINE depth does.
+ *   (ciphertext.rs:476-535), as the per-token LoRA pass (encrypt, ct x pt,
+ *   rescale, decrypt) does.
  * TH_LORA_SK_FUSED: the decryption-fused shortcut. Without it (the default)
  *   the token runs the reference's client/server sequence
  *   (inference_engine.py:1477-1482): encrypt_pk forms every limb of c0 and c1

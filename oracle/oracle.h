@@ -1,8 +1,9 @@
 // CPU oracle: a C++ restatement of the reference CPU CKKS backend
 // (tensafe-he/crates/tensafe-he-core/src/*.rs).
 //
-// TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP engine in
-// provenloop_amd/ and the timed host-CPU baseline of bench.py. It is never
+// TEST INFRASTRUCTURE ONLY. This library gives the results the tests of the
+// HIP engine in provenloop_amd/ compare against, and the timed host-CPU
+// baseline of bench.py. It is never
 // linked into, loaded by, or called from the product path.
 //
 // Every function follows the reference line by line (same algorithm, same

@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. The oracle is a C++ restatement of the reference CPU
 CKKS backend (tensafe-he/crates/tensafe-he-core/src/*.rs). It is imported only
 by tests/, by ``__graft_entry__.smoke()`` and by bench.py's CPU-baseline leg,
-always as the checker or the timed baseline, never as the thing measured or
-shipped. The product path (provenloop_amd) never imports this module.
+always as the source of expected results or the timed baseline, never as the
+thing measured or shipped. The product path (provenloop_amd) never imports this module.
 """
 from __future__ import annotations
 

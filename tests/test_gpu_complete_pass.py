@@ -11,7 +11,7 @@ compared with the oracle's composed operations bit for bit: the encrypt_pk
 output of each input, and every batch's product (rescaled or not). The
 token's segment sums equal those of the sk-fused shortcut bit for bit (the
 same residues on the limbs a decryption reads), and its deltas match the
-oracle within the north-star bound.
+oracle within the 1e-3 relative bound on decoded deltas.
 """
 import numpy as np
 import pytest

@@ -6,7 +6,7 @@ The oracle side composes the reference operations one by one
 the replicated input, ct x pt with each packed batch, rescale, decrypt, sum
 of each d-slot segment, then B @ intermediate. Segment sums are reduced in a
 different order on the GPU, so they are held to 1e-9 absolute (relative to
-their size) and the deltas to the north-star 1e-3 relative bound (in
+their size) and the deltas to the 1e-3 relative bound on decoded deltas (in
 practice ~1e-15); the ciphertext arithmetic under them is bit-exact (see
 test_gpu_parity.py), and the set's segment sums equal th_lora_a_pass's bit
 for bit.

@@ -5,7 +5,7 @@ ciphertexts, serialised bytes) must equal the oracle's exactly; decrypted
 slots come from an f64 decode evaluated in the reference's order with the
 reference's twiddles, so they must be bit-identical too. The LoRA segment
 sums are reduced in a different order than numpy's, so they are held to the
-north-star bound ||gpu - cpu|| / ||cpu|| <= 1e-3 (in practice ~1e-15).
+bound on decoded deltas ||gpu - cpu|| / ||cpu|| <= 1e-3 (in practice ~1e-15).
 """
 import numpy as np
 import pytest
