@@ -60,7 +60,7 @@ class _Handle:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and _lib._lib is not None:
+        if h and getattr(_lib, "_lib", None) is not None:
             getattr(_lib._lib, self._free_fn)(h)
             self._h = None
 
@@ -155,7 +155,7 @@ class CkksContext:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and _lib._lib is not None:
+        if h and getattr(_lib, "_lib", None) is not None:
             _lib._lib.th_ctx_free(h)
             self._h = None
 

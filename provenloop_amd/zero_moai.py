@@ -204,7 +204,7 @@ class LoraSet:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and _lib._lib is not None:
+        if h and getattr(_lib, "_lib", None) is not None:
             _lib._lib.th_lora_free(h)
             self._h = None
 
