@@ -282,26 +282,52 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
 #pragma unroll
     for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gdst[jbase + p1(k)]);
-    // The store's operands are loaded behind the intermediate, before the
-    // butterflies, and combined after the first stages, so their latency
-    // overlaps the arithmetic.
-    constexpr int NP = SOp::NAUX > 0 ? 16 : 1;
-    typename SOp::Aux v[NP];
-    uint64_t c[NP];
     if constexpr (SOp::NAUX > 0) {
+      // The store's operands and outputs in pairs of adjacent positions per
+      // lane: register k is position h(k) = 2 lane + (k & 1) + 128 (k >> 1)
+      // of the part, so they move as 16-byte accesses, half the memory
+      // instructions of the lane-contiguous layout (this pass is bound by
+      // the CUs' vector-memory address processing more than by its
+      // arithmetic). The operands are loaded behind the intermediate,
+      // before the butterflies, and combined after the first stages, so
+      // their latency overlaps the arithmetic.
+      auto h = [&](uint32_t k) { return (l << 1) + (k & 1) + ((k >> 1) << 7); };
+      using U2 = uint64_t __attribute__((ext_vector_type(2)));
+      typename SOp::Aux v[16];
+      uint64_t c[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = so.load_aux(jbase + g(k));
-    }
-    fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, (SOp::NAUX > 0)>(x, jbase + p1(0), tw, ar);
-    wave_exchange(x, lds, p1, p2);
-    if constexpr (SOp::NAUX > 0) {
+      for (int k = 0; k < 16; k += 2) {
+        const U2 a = ((GPtr<U2>)gld(so.aux))[(jbase + h(k)) >> 1];
+        v[k].a = a.x;
+        v[k + 1].a = a.y;
+        if constexpr (SOp::NAUX >= 2) {
+          const U2 b = ((GPtr<U2>)gld(so.aux2))[(jbase + h(k)) >> 1];
+          v[k].b = b.x;
+          v[k + 1].b = b.y;
+        }
+      }
+      fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), tw, ar);
+      wave_exchange(x, lds, p1, p2);
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
-    }
-    fwd_stages<LOGN, 0, CB - 5, 0, A, (SOp::NAUX > 0)>(x, jbase + p2(0), tw, ar);
-    wave_exchange(x, lds, p2, g);
+      fwd_stages<LOGN, 0, CB - 5, 0, A, true>(x, jbase + p2(0), tw, ar);
+      wave_exchange(x, lds, p2, h);
+      const GMut<U2> d2 = (GMut<U2>)gdst;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) so.store(ar, x[k], gdst, jbase + g(k), c[NP > 1 ? k : 0]);
+      for (int k = 0; k < 16; k += 2) {
+        U2 o;
+        o.x = so.apply_prep(ar, x[k], c[k]);
+        o.y = so.apply_prep(ar, x[k + 1], c[k + 1]);
+        d2[(jbase + h(k)) >> 1] = o;
+      }
+    } else {
+      fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, false>(x, jbase + p1(0), tw, ar);
+      wave_exchange(x, lds, p1, p2);
+      fwd_stages<LOGN, 0, CB - 5, 0, A, false>(x, jbase + p2(0), tw, ar);
+      wave_exchange(x, lds, p2, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) so.store(ar, x[k], gdst, jbase + g(k), 0);
+    }
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
     if constexpr (LOp::kind == NTT_LOAD_MULM) {
