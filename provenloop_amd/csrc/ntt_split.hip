@@ -51,6 +51,9 @@ struct Split {
   static constexpr int PARTS = N >> 10;          // wavefronts per limb-polynomial
   static constexpr int CW = 1 << (10 - RB);      // columns per column-pass wavefront
   static constexpr int LDS = 1024 + 64;          // one padding word per 16
+  // twiddle entries of a row-pass wavefront's first register pass (stages
+  // CB-1 .. CB-4: 2^(9-b) entries of stage b over its 2^(10-CB) rows)
+  static constexpr int TW1 = 15 << (10 - CB);
   static_assert(CB >= 4 && RB >= 4 && RB <= 10 && CB <= 10, "unsupported split");
 };
 
@@ -66,9 +69,9 @@ __device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
 // inv_stages); the plain forward column and row passes keep the compiler's
 // schedule, which measured faster there (N=32768 forward row pass 35.0
 // against 36.1 us).
-template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = true>
-__device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
-                                           const A& ar) {
+// The twiddles come from get(b, i), the table entry i of stage b.
+template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH, class Get>
+__device__ __forceinline__ void fwd_stages_get(typename A::V (&x)[16], uint32_t f, const Get& get, const A& ar) {
 #pragma unroll
   for (int b = BHI; b >= BLO; --b) {
     const int rb = b - EB;
@@ -78,7 +81,7 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, G
       typename A::Tw t[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        if (j < (16 >> (rb + 1))) t[j] = ld16(tw, base | (uint32_t)j);
+        if (j < (16 >> (rb + 1))) t[j] = get(b, base | (uint32_t)j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
@@ -89,11 +92,16 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, G
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         if (k & (1 << rb)) continue;
-        const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
+        const typename A::Tw t = get(b, base | (uint32_t)(k >> (rb + 1)));
         ar.fwd(x[k], x[k | (1 << rb)], t);
       }
     }
   }
+}
+template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = true>
+__device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
+                                           const A& ar) {
+  fwd_stages_get<LOGN, EB, BHI, BLO, A, BATCH>(x, f, [&](int, uint32_t i) { return ld16(tw, i); }, ar);
 }
 
 // Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
@@ -306,7 +314,28 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
           v[k + 1].b = b.y;
         }
       }
-      fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), tw, ar);
+      // The first register pass's twiddles are shared by the lanes of a row
+      // (2^(CB-4) lanes): the wavefront loads each of them once into LDS,
+      // entry e at stage b = CB - 1 - s with s = log2(e / 2^(10-CB) + 1),
+      // and the lanes read them there.
+      using Tw = typename A::Tw;
+      Tw* tl = reinterpret_cast<Tw*>(lds_raw + S::LDS);
+      const uint32_t nj = (1u << LOGN) | jbase;
+#pragma unroll
+      for (int r = 0; r < (S::TW1 + 63) / 64; ++r) {
+        const uint32_t e = l + 64u * r;
+        if (e < (uint32_t)S::TW1) {
+          const uint32_t s = 31u - (uint32_t)__builtin_clz((e >> (10 - CB)) + 1);
+          const uint32_t b = CB - 1 - s;
+          tl[e] = ld16(tw, (nj >> (b + 1)) + e - (((1u << s) - 1) << (10 - CB)));
+        }
+      }
+      slice_sync();
+      auto get = [&](int b, uint32_t i) {
+        const int s = CB - 1 - b;
+        return tl[(((1u << s) - 1) << (10 - CB)) + i - (nj >> (b + 1))];
+      };
+      fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), get, ar);
       wave_exchange(x, lds, p1, p2);
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
@@ -372,7 +401,9 @@ __device__ __forceinline__ uint32_t column_part(uint32_t p) {
 template <int LOGN, bool INV, bool COLUMN, uint32_t LD, uint32_t ST>
 __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
-  __shared__ uint64_t lds[S::LDS];
+  // the forward row pass with a fused rescale store also holds its first
+  // register pass's twiddles (16-byte entries)
+  __shared__ uint64_t lds[S::LDS + (!INV && !COLUMN && StoreOp<ST>::NAUX > 0 ? 2 * S::TW1 : 0)];
   const uint32_t job = blockIdx.x / S::PARTS;
   uint32_t part = blockIdx.x % S::PARTS;
   if constexpr (COLUMN) part = column_part<LOGN>(part);
