@@ -54,6 +54,9 @@ struct Split {
   // twiddle entries of a row-pass wavefront's first register pass (stages
   // CB-1 .. CB-4: 2^(9-b) entries of stage b over its 2^(10-CB) rows)
   static constexpr int TW1 = 15 << (10 - CB);
+  // and of an inverse row-pass wavefront's second register pass (stages 4 ..
+  // CB-1)
+  static constexpr int TWI = ((1 << (CB - 4)) - 1) << (10 - CB);
   static_assert(CB >= 4 && RB >= 4 && RB <= 10 && CB <= 10, "unsupported split");
 };
 
@@ -107,9 +110,10 @@ __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, G
 // Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
 // With BATCH, as in fwd_stages, each stage's twiddles are requested before
 // its first butterfly.
-template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH = true>
-__device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
-                                           const A& ar, const LimbConst& lc) {
+// The twiddles come from get(b, i), the table entry i of stage b.
+template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH, class Get>
+__device__ __forceinline__ void inv_stages_get(typename A::V (&x)[16], uint32_t f, const Get& get, const A& ar,
+                                               const LimbConst& lc) {
 #pragma unroll
   for (int b = BLO; b <= BHI; ++b) {
     const int rb = b - EB;
@@ -123,7 +127,7 @@ __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, G
       typename A::Tw t[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        if (j < (16 >> (rb + 1))) t[j] = ld16(tw, base | (uint32_t)j);
+        if (j < (16 >> (rb + 1))) t[j] = get(b, base | (uint32_t)j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k)
@@ -132,7 +136,7 @@ __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, G
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         if (k & (1 << rb)) continue;
-        const typename A::Tw t = ld16(tw, base | (uint32_t)(k >> (rb + 1)));
+        const typename A::Tw t = get(b, base | (uint32_t)(k >> (rb + 1)));
         ar.inv(x[k], x[k | (1 << rb)], t);
       }
     }
@@ -141,6 +145,11 @@ __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, G
 #pragma unroll
     for (int k = 0; k < 16; ++k) ar.inv_pass_end(x[k]);
   }
+}
+template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH = true>
+__device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
+                                           const A& ar, const LimbConst& lc) {
+  inv_stages_get<LOGN, EB, BLO, BHI, A, BATCH>(x, f, [&](int, uint32_t i) { return ld16(tw, i); }, ar, lc);
 }
 
 // Re-distribute the wavefront's 16 x 64 coefficients from layout `from` to
@@ -360,20 +369,53 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
   } else {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
     if constexpr (LOp::kind == NTT_LOAD_MULM) {
-      // all 32 operand loads in flight before the first product
+      // The product's operands in pairs of adjacent positions per lane (the
+      // layout h of the forward pass with a fused store: 16-byte loads, half
+      // the memory instructions), all in flight before the first product.
+      auto h = [&](uint32_t k) { return (l << 1) + (k & 1) + ((k >> 1) << 7); };
+      using U2 = uint64_t __attribute__((ext_vector_type(2)));
+      const GPtr<U2> s2 = (const GPtr<U2>)gld(src), a2 = (const GPtr<U2>)gld(op.aux);
       typename LOp::Raw r[16];
-      op.fetch16(src, [&](int k) { return jbase + g(k); }, r);
+#pragma unroll
+      for (int k = 0; k < 16; k += 2) {
+        const U2 s = s2[(jbase + h(k)) >> 1], a = a2[(jbase + h(k)) >> 1];
+        r[k] = typename LOp::Raw{s.x, a.x};
+        r[k + 1] = typename LOp::Raw{s.y, a.y};
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op.finish(r[k]));
+      // the second register pass's twiddles are shared by the lanes of a
+      // row: loaded once per wavefront into LDS (the forward pass's table
+      // layout, stages CB - 1 down to 4)
+      using Tw = typename A::Tw;
+      Tw* tl = reinterpret_cast<Tw*>(lds_raw + S::LDS);
+      const uint32_t nj = (1u << LOGN) | jbase;
+#pragma unroll
+      for (int rr = 0; rr < (S::TWI + 63) / 64; ++rr) {
+        const uint32_t e = l + 64u * rr;
+        if (e < (uint32_t)S::TWI) {
+          const uint32_t s = 31u - (uint32_t)__builtin_clz((e >> (10 - CB)) + 1);
+          const uint32_t b = CB - 1 - s;
+          tl[e] = ld16(tw, (nj >> (b + 1)) + e - (((1u << s) - 1) << (10 - CB)));
+        }
+      }
+      wave_exchange(x, lds, h, p2);
+      inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+      wave_exchange(x, lds, p2, p1);
+      auto get = [&](int b, uint32_t i) {
+        const int s = CB - 1 - b;
+        return tl[(((1u << s) - 1) << (10 - CB)) + i - (nj >> (b + 1))];
+      };
+      inv_stages_get<LOGN, CB - 4, 4, CB - 1, A, true>(x, jbase + p1(0), get, ar, lc);
     } else {
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
+      wave_exchange(x, lds, g, p2);
+      inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+      wave_exchange(x, lds, p2, p1);
+      inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
     }
-    wave_exchange(x, lds, g, p2);
-    inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
-    wave_exchange(x, lds, p2, p1);
-    inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
 #pragma unroll
     for (int k = 0; k < 16; ++k) gdst[jbase + p1(k)] = ar.raw(x[k]);
   }
@@ -401,9 +443,13 @@ __device__ __forceinline__ uint32_t column_part(uint32_t p) {
 template <int LOGN, bool INV, bool COLUMN, uint32_t LD, uint32_t ST>
 __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
-  // the forward row pass with a fused rescale store also holds its first
-  // register pass's twiddles (16-byte entries)
-  __shared__ uint64_t lds[S::LDS + (!INV && !COLUMN && StoreOp<ST>::NAUX > 0 ? 2 * S::TW1 : 0)];
+  // the forward row pass with a fused rescale store, and the inverse row pass
+  // with the product in its loads, also hold one register pass's twiddles
+  // (16-byte entries)
+  __shared__ uint64_t lds[S::LDS + (COLUMN                                   ? 0
+                                    : !INV && StoreOp<ST>::NAUX > 0          ? 2 * S::TW1
+                                    : INV && LD == NTT_LOAD_MULM             ? 2 * S::TWI
+                                                                             : 0)];
   const uint32_t job = blockIdx.x / S::PARTS;
   uint32_t part = blockIdx.x % S::PARTS;
   if constexpr (COLUMN) part = column_part<LOGN>(part);
