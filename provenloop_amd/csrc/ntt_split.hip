@@ -203,7 +203,10 @@ __device__ __forceinline__ void column_fwd_regs(typename A::V (&x)[16], uint64_t
   const GMut<uint64_t> gdst = gst(dst);
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
-  fwd_stages<LOGN, LOGN - 4, LOGN - 1, LOGN - 4, A, BATCH>(x, m.j1(0), tw, ar);
+  // stages on bits >= LOGN - 4 (the Q1 registers): every lane's element
+  // bits above the stage are zero, so the twiddle index is uniform (f = 0)
+  fwd_stages_get<LOGN, LOGN - 4, LOGN - 1, LOGN - 4, A, BATCH>(
+      x, 0u, [&](int, uint32_t i) { return ld16_uniform(tw, i); }, ar);
   wave_exchange(x, lds, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
   fwd_stages<LOGN, CB, LOGN - 5, CB, A, BATCH>(x, m.j2(0), tw, ar);
 #pragma unroll
@@ -223,7 +226,11 @@ __device__ __forceinline__ void column_inv_regs(typename A::V (&x)[16], const ui
   for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gbuf[m.j2(k)]);
   inv_stages<LOGN, CB, CB, CB + 3>(x, m.j2(0), tw, ar, lc);
   wave_exchange(x, lds, [&](uint32_t k) { return m.e2(k); }, [&](uint32_t k) { return m.e1(k); });
-  inv_stages<LOGN, LOGN - 4, CB + 4, LOGN - 1>(x, m.j1(0), tw, ar, lc);
+  // stages CB + 4 .. LOGN - 1 on the Q1 registers (bits LOGN - 4 ..): uniform
+  // twiddle indices, as in column_fwd_regs
+  static_assert(CB + 4 >= LOGN - 4, "the second inverse column pass must lie in the Q1 register bits");
+  inv_stages_get<LOGN, LOGN - 4, CB + 4, LOGN - 1, A, true>(
+      x, 0u, [&](int, uint32_t i) { return ld16_uniform(tw, i); }, ar, lc);
 }
 
 template <int LOGN, bool INV, class A, class LOp>

@@ -93,6 +93,17 @@ __device__ __forceinline__ T ld16(GPtr<T> p, uint32_t i) {
   using V = uint64_t __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(T, ((GPtr<V>)p)[i]);
 }
+// The same through the constant address space, for an index that is the same
+// on every lane of the wavefront: a scalar load, which leaves the CU's
+// vector-memory path to the per-lane accesses (only for tables that no kernel
+// writes while it runs).
+template <class T>
+__device__ __forceinline__ T ld16_uniform(GPtr<T> p, uint32_t i) {
+  static_assert(sizeof(T) == 16, "16-byte records only");
+  using V = uint64_t __attribute__((ext_vector_type(2)));
+  using CPtr = const __attribute__((address_space(4))) V*;
+  return __builtin_bit_cast(T, ((CPtr)(const void*)p)[__builtin_amdgcn_readfirstlane(i)]);
+}
 
 // floor(x * s / 2^64) - e with e in {0, 1, 2}: x1*s1 + hi(x1*s0) + hi(x0*s1)
 // for 32-bit halves; the low halves of the two cross products and hi(x0*s0)
