@@ -45,7 +45,6 @@
 
 namespace th {
 
-constexpr int NTT_SPLIT_MIN_LOGN = 13;
 constexpr int NTT_WHOLE_MAX_LOGN = 14;
 #ifndef NTT_WHOLE_MAX_JOBS
 #define NTT_WHOLE_MAX_JOBS 256

@@ -45,7 +45,7 @@ namespace th {
 template <int LOGN>
 struct Split {
   static constexpr int N = 1 << LOGN;
-  static constexpr int CB = LOGN >= 15 ? 8 : 7;  // column bits
+  static constexpr int CB = split_column_bits(LOGN);  // column bits
   static constexpr int RB = LOGN - CB;           // row bits
   static constexpr int E = 16;
   static constexpr int PARTS = N >> 10;          // wavefronts per limb-polynomial
@@ -72,7 +72,8 @@ __device__ __forceinline__ uint32_t pad16(uint32_t e) { return e + (e >> 4); }
 // inv_stages); the plain forward column and row passes keep the compiler's
 // schedule, which measured faster there (N=32768 forward row pass 35.0
 // against 36.1 us).
-// The twiddles come from get(b, i), the table entry i of stage b.
+// The twiddles come from get(b, base, s): entry base | s of stage b's table
+// (s = the slot of the register pair among the stage's twiddles of the lane).
 template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH, class Get>
 __device__ __forceinline__ void fwd_stages_get(typename A::V (&x)[16], uint32_t f, const Get& get, const A& ar) {
 #pragma unroll
@@ -84,7 +85,7 @@ __device__ __forceinline__ void fwd_stages_get(typename A::V (&x)[16], uint32_t 
       typename A::Tw t[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        if (j < (16 >> (rb + 1))) t[j] = get(b, base | (uint32_t)j);
+        if (j < (16 >> (rb + 1))) t[j] = get(b, base, (uint32_t)j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
@@ -95,7 +96,7 @@ __device__ __forceinline__ void fwd_stages_get(typename A::V (&x)[16], uint32_t 
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         if (k & (1 << rb)) continue;
-        const typename A::Tw t = get(b, base | (uint32_t)(k >> (rb + 1)));
+        const typename A::Tw t = get(b, base, (uint32_t)(k >> (rb + 1)));
         ar.fwd(x[k], x[k | (1 << rb)], t);
       }
     }
@@ -104,13 +105,14 @@ __device__ __forceinline__ void fwd_stages_get(typename A::V (&x)[16], uint32_t 
 template <int LOGN, int EB, int BHI, int BLO, class A, bool BATCH = true>
 __device__ __forceinline__ void fwd_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar) {
-  fwd_stages_get<LOGN, EB, BHI, BLO, A, BATCH>(x, f, [&](int, uint32_t i) { return ld16(tw, i); }, ar);
+  fwd_stages_get<LOGN, EB, BHI, BLO, A, BATCH>(x, f, [&](int, uint32_t base, uint32_t s) { return ld16(tw, base | s); },
+                                               ar);
 }
 
 // Inverse stages BLO up to BHI; the stage on bit LOGN-1 folds in N^{-1}.
 // With BATCH, as in fwd_stages, each stage's twiddles are requested before
 // its first butterfly.
-// The twiddles come from get(b, i), the table entry i of stage b.
+// The twiddles come from get(b, base, s), as in fwd_stages_get.
 template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH, class Get>
 __device__ __forceinline__ void inv_stages_get(typename A::V (&x)[16], uint32_t f, const Get& get, const A& ar,
                                                const LimbConst& lc) {
@@ -127,7 +129,7 @@ __device__ __forceinline__ void inv_stages_get(typename A::V (&x)[16], uint32_t 
       typename A::Tw t[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        if (j < (16 >> (rb + 1))) t[j] = get(b, base | (uint32_t)j);
+        if (j < (16 >> (rb + 1))) t[j] = get(b, base, (uint32_t)j);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k)
@@ -136,7 +138,7 @@ __device__ __forceinline__ void inv_stages_get(typename A::V (&x)[16], uint32_t 
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         if (k & (1 << rb)) continue;
-        const typename A::Tw t = get(b, base | (uint32_t)(k >> (rb + 1)));
+        const typename A::Tw t = get(b, base, (uint32_t)(k >> (rb + 1)));
         ar.inv(x[k], x[k | (1 << rb)], t);
       }
     }
@@ -149,7 +151,8 @@ __device__ __forceinline__ void inv_stages_get(typename A::V (&x)[16], uint32_t 
 template <int LOGN, int EB, int BLO, int BHI, class A, bool BATCH = true>
 __device__ __forceinline__ void inv_stages(typename A::V (&x)[16], uint32_t f, GPtr<typename A::Tw> tw,
                                            const A& ar, const LimbConst& lc) {
-  inv_stages_get<LOGN, EB, BLO, BHI, A, BATCH>(x, f, [&](int, uint32_t i) { return ld16(tw, i); }, ar, lc);
+  inv_stages_get<LOGN, EB, BLO, BHI, A, BATCH>(x, f, [&](int, uint32_t base, uint32_t s) { return ld16(tw, base | s); },
+                                               ar, lc);
 }
 
 // Re-distribute the wavefront's 16 x 64 coefficients from layout `from` to
@@ -206,7 +209,7 @@ __device__ __forceinline__ void column_fwd_regs(typename A::V (&x)[16], uint64_t
   // stages on bits >= LOGN - 4 (the Q1 registers): every lane's element
   // bits above the stage are zero, so the twiddle index is uniform (f = 0)
   fwd_stages_get<LOGN, LOGN - 4, LOGN - 1, LOGN - 4, A, BATCH>(
-      x, 0u, [&](int, uint32_t i) { return ld16_uniform(tw, i); }, ar);
+      x, 0u, [&](int, uint32_t base, uint32_t s) { return ld16_uniform(tw, base | s); }, ar);
   wave_exchange(x, lds, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
   fwd_stages<LOGN, CB, LOGN - 5, CB, A, BATCH>(x, m.j2(0), tw, ar);
 #pragma unroll
@@ -230,7 +233,7 @@ __device__ __forceinline__ void column_inv_regs(typename A::V (&x)[16], const ui
   // twiddle indices, as in column_fwd_regs
   static_assert(CB + 4 >= LOGN - 4, "the second inverse column pass must lie in the Q1 register bits");
   inv_stages_get<LOGN, LOGN - 4, CB + 4, LOGN - 1, A, true>(
-      x, 0u, [&](int, uint32_t i) { return ld16_uniform(tw, i); }, ar, lc);
+      x, 0u, [&](int, uint32_t base, uint32_t s) { return ld16_uniform(tw, base | s); }, ar, lc);
 }
 
 template <int LOGN, bool INV, class A, class LOp>
@@ -302,6 +305,12 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
   const GMut<uint64_t> gdst = gst(dst);
   typename A::V x[16];
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
+  // the stages on the P2 register bits (bits 0..3, every lane its own
+  // twiddles) read the row table, one load of consecutive entries per slot
+  auto row_get = [&](const void* table) {
+    const GPtr<typename A::Tw> tr = gld(reinterpret_cast<const typename A::Tw*>(table));
+    return [=](int b, uint32_t, uint32_t s) { return ld16(tr, row_table_index(S::N, b, part, s, l)); };
+  };
   if constexpr (!INV) {
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
 #pragma unroll
@@ -347,15 +356,15 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
         }
       }
       slice_sync();
-      auto get = [&](int b, uint32_t i) {
+      auto get = [&](int b, uint32_t base, uint32_t j) {
         const int s = CB - 1 - b;
-        return tl[(((1u << s) - 1) << (10 - CB)) + i - (nj >> (b + 1))];
+        return tl[(((1u << s) - 1) << (10 - CB)) + (base | j) - (nj >> (b + 1))];
       };
       fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), get, ar);
       wave_exchange(x, lds, p1, p2);
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
-      fwd_stages<LOGN, 0, CB - 5, 0, A, true>(x, jbase + p2(0), tw, ar);
+      fwd_stages_get<LOGN, 0, CB - 5, 0, A, true>(x, jbase + p2(0), row_get(lc.fwd_row), ar);
       wave_exchange(x, lds, p2, h);
       const GMut<U2> d2 = (GMut<U2>)gdst;
 #pragma unroll
@@ -368,7 +377,7 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
     } else {
       fwd_stages<LOGN, CB - 4, CB - 1, CB - 4, A, false>(x, jbase + p1(0), tw, ar);
       wave_exchange(x, lds, p1, p2);
-      fwd_stages<LOGN, 0, CB - 5, 0, A, false>(x, jbase + p2(0), tw, ar);
+      fwd_stages_get<LOGN, 0, CB - 5, 0, A, false>(x, jbase + p2(0), row_get(lc.fwd_row), ar);
       wave_exchange(x, lds, p2, g);
 #pragma unroll
       for (int k = 0; k < 16; ++k) so.store(ar, x[k], gdst, jbase + g(k), 0);
@@ -408,18 +417,18 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
         }
       }
       wave_exchange(x, lds, h, p2);
-      inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+      inv_stages_get<LOGN, 0, 0, 3, A, true>(x, jbase + p2(0), row_get(lc.inv_row), ar, lc);
       wave_exchange(x, lds, p2, p1);
-      auto get = [&](int b, uint32_t i) {
+      auto get = [&](int b, uint32_t base, uint32_t j) {
         const int s = CB - 1 - b;
-        return tl[(((1u << s) - 1) << (10 - CB)) + i - (nj >> (b + 1))];
+        return tl[(((1u << s) - 1) << (10 - CB)) + (base | j) - (nj >> (b + 1))];
       };
       inv_stages_get<LOGN, CB - 4, 4, CB - 1, A, true>(x, jbase + p1(0), get, ar, lc);
     } else {
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
       wave_exchange(x, lds, g, p2);
-      inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+      inv_stages_get<LOGN, 0, 0, 3, A, true>(x, jbase + p2(0), row_get(lc.inv_row), ar, lc);
       wave_exchange(x, lds, p2, p1);
       inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
     }

@@ -185,8 +185,13 @@ void build_tables(th_ctx* c) {
   const uint32_t N = c->N, L = c->L;
   std::vector<BarrettConst> bc(L);
   c->h_lc.resize(L);
-  // twiddles: per limb forward then inverse, N pairs of 16 bytes each
-  const size_t tab_bytes = (size_t)L * 2 * N * 16;
+  // twiddles: per limb forward then inverse, N pairs of 16 bytes each; at the
+  // split kernels' sizes followed by the row tables (row_table_index), per
+  // limb forward then inverse, 15 N / 16 pairs each
+  const bool split = c->logn >= (uint32_t)NTT_SPLIT_MIN_LOGN && c->logn <= (uint32_t)NTT_MAX_LOGN;
+  const size_t row_n = split ? (size_t)15 * N / 16 : 0;
+  const size_t main_bytes = (size_t)L * 2 * N * 16;
+  const size_t tab_bytes = main_bytes + (size_t)L * 2 * row_n * 16;
   HIPCHK(hipMalloc(&c->d_tables, tab_bytes));
   std::vector<uint64_t> fw(N), iw(N);
   std::vector<unsigned char> host_tab(tab_bytes);
@@ -217,6 +222,19 @@ void build_tables(th_ctx* c) {
         memcpy(idst + 16 * (size_t)i, &b, 16);
       }
     }
+    unsigned char* frow = host_tab.data() + main_bytes + (size_t)(2 * l) * row_n * 16;
+    unsigned char* irow = host_tab.data() + main_bytes + (size_t)(2 * l + 1) * row_n * 16;
+    if (split) {
+      const uint32_t parts = N >> 10;
+      for (int b = 0; b < 4; ++b)
+        for (uint32_t p = 0; p < parts; ++p)
+          for (uint32_t s = 0; s < (16u >> (b + 1)); ++s)
+            for (uint32_t ln = 0; ln < 64; ++ln) {
+              const uint32_t to = row_table_index(N, b, p, s, ln), from = row_table_source(N, (int)c->logn, b, p, s, ln);
+              memcpy(frow + 16 * (size_t)to, fdst + 16 * (size_t)from, 16);
+              memcpy(irow + 16 * (size_t)to, idst + 16 * (size_t)from, 16);
+            }
+    }
     LimbConst& lc = c->h_lc[l];
     memset(&lc, 0, sizeof(lc));
     lc.q = q;
@@ -233,6 +251,8 @@ void build_tables(th_ctx* c) {
     lc.last_wdq = (double)lc.last_w / (double)q;
     lc.fwd = (const char*)c->d_tables + (size_t)(2 * l) * N * 16;
     lc.inv = (const char*)c->d_tables + (size_t)(2 * l + 1) * N * 16;
+    lc.fwd_row = split ? (const char*)c->d_tables + main_bytes + (size_t)(2 * l) * row_n * 16 : nullptr;
+    lc.inv_row = split ? (const char*)c->d_tables + main_bytes + (size_t)(2 * l + 1) * row_n * 16 : nullptr;
     lc.fp64 = fp ? 1 : 0;
     const u128 r = (~(u128)0) / q;
     uint64_t qi = 1;  // q^{-1} mod 2^64 by Newton's iteration (each step doubles the correct bits)

@@ -40,6 +40,8 @@ struct LimbConst {
   double last_wd, last_wdq;
   const void* fwd;            // N twiddle pairs (ShoupTw or Fp64Tw), fwd[brv(i)] = psi^i
   const void* inv;            // N twiddle pairs, inv[brv(i)] = psi^-i
+  const void* fwd_row;        // fwd and inv entries of the split row passes' lane-bit stages
+  const void* inv_row;        //   in the order their lanes read them (row_table_index)
   uint32_t fp64;              // 1 if this limb uses the fp64 path
   uint32_t pad_;
 };

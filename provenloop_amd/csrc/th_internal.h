@@ -197,5 +197,28 @@ hipError_t launch_decrypt_sums_split(int logn, const NttArgs& row, const Rescale
 // Supported transform sizes.
 constexpr int NTT_MIN_LOGN = 10;
 constexpr int NTT_MAX_LOGN = 15;
+// Transform sizes of the split kernels, and their column bits CB: the index
+// j = (row << CB) | col of a coefficient, column passes over the row bits and
+// row passes over the column bits (1024 coefficients per wavefront).
+constexpr int NTT_SPLIT_MIN_LOGN = 13;
+__host__ __device__ constexpr int split_column_bits(int logn) { return logn >= 15 ? 8 : 7; }
+// Row-pass twiddle tables (LimbConst::fwd_row, inv_row): the row passes' stages
+// on bits b = 0..3, where each lane holds its own elements, read entry
+// ((N | j) >> (b + 1)) of the table for slot s = 0 .. (16 >> (b + 1)) - 1 of
+// lane l in wavefront part p, with j = p 1024 + (s << (b + 1)) + ((l mod 2^(CB-4))
+// << 4) + ((l >> (CB - 4)) << CB). The row table holds those entries stage by
+// stage (stage b from N - (N >> b), N >> (b + 1) entries) in the order
+// (p, s, l), so that a load instruction of the 64 lanes reads 1 KiB of
+// consecutive entries: 15 N / 16 entries per direction.
+__host__ __device__ constexpr uint32_t row_table_index(uint32_t n, int b, uint32_t part, uint32_t s, uint32_t lane) {
+  return n - (n >> b) + ((part * (16u >> (b + 1)) + s) << 6) + lane;
+}
+__host__ __device__ constexpr uint32_t row_table_source(uint32_t n, int logn, int b, uint32_t part, uint32_t s,
+                                                        uint32_t lane) {
+  const int cb = split_column_bits(logn);
+  const uint32_t j = (part << 10) + (s << (b + 1)) + ((lane & ((1u << (cb - 4)) - 1)) << 4) +
+                     ((lane >> (cb - 4)) << cb);
+  return (n | j) >> (b + 1);
+}
 
 }  // namespace th
