@@ -264,6 +264,37 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
 }
 
 // ------------------------------------------------------------------ row pass
+// The twiddles of a row-pass register pass on the P1 bits (stages CB - 1 down
+// to CB - 4, or the inverse pass's 4 .. CB - 1) are shared by the 2^(CB-4)
+// lanes of a row: a workgroup can load each of them once into LDS and let
+// the lanes read them there. Entry e holds stage b = CB - 1 - s, with
+// s = log2(e / 2^(10-CB) + 1); stage b's entries of part jbase / 1024 are
+// those of index base | j in the twiddle table, base >= nj >> (b + 1).
+template <int LOGN, class Tw>
+struct RowStage {
+  static constexpr int CB = Split<LOGN>::CB;
+  Tw* tl;
+  uint32_t nj;
+  __device__ RowStage(Tw* t, uint32_t jbase) : tl(t), nj((1u << LOGN) | jbase) {}
+  // entries t, t + STRIDE, ... below COUNT, by thread t of STRIDE
+  template <int COUNT, int STRIDE>
+  __device__ void fill(const GPtr<Tw>& tw, uint32_t t) const {
+#pragma unroll
+    for (int r = 0; r < (COUNT + STRIDE - 1) / STRIDE; ++r) {
+      const uint32_t e = t + (uint32_t)STRIDE * r;
+      if (e < (uint32_t)COUNT) {
+        const uint32_t s = 31u - (uint32_t)__builtin_clz((e >> (10 - CB)) + 1);
+        const uint32_t b = CB - 1 - s;
+        tl[e] = ld16(tw, (nj >> (b + 1)) + e - (((1u << s) - 1) << (10 - CB)));
+      }
+    }
+  }
+  __device__ Tw operator()(int b, uint32_t base, uint32_t j) const {
+    const int s = CB - 1 - b;
+    return tl[(((1u << s) - 1) << (10 - CB)) + (base | j) - (nj >> (b + 1))];
+  }
+};
+
 // Forward row pass of part `part` from the column pass's intermediate in buf;
 // leaves the transform's outputs (the arithmetic's representation) in
 // registers in the lane-contiguous layout G: x[k] is element part * 1024 +
@@ -281,11 +312,16 @@ __device__ __forceinline__ void row_fwd_regs(typename A::V (&x)[16], const uint6
   typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   const GPtr<uint64_t> gbuf = gld(buf);
   const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
+  const GPtr<typename A::Tw> tr = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd_row));
 #pragma unroll
   for (int k = 0; k < 16; ++k) x[k] = ar.unraw(gbuf[jbase + p1(k)]);
   fwd_stages<LOGN, CB - 4, CB - 1, CB - 4>(x, jbase + p1(0), tw, ar);
   wave_exchange(x, lds, p1, p2);
-  fwd_stages<LOGN, 0, CB - 5, 0>(x, jbase + p2(0), tw, ar);
+  // the stages on the P2 register bits read the row table (one load of
+  // consecutive entries per slot)
+  fwd_stages_get<LOGN, 0, CB - 5, 0, A, true>(
+      x, jbase + p2(0),
+      [&](int b, uint32_t, uint32_t s) { return ld16(tr, row_table_index(Split<LOGN>::N, b, part, s, l)); }, ar);
   wave_exchange(x, lds, p2, g);
 }
 
@@ -339,28 +375,11 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
           v[k + 1].b = b.y;
         }
       }
-      // The first register pass's twiddles are shared by the lanes of a row
-      // (2^(CB-4) lanes): the wavefront loads each of them once into LDS,
-      // entry e at stage b = CB - 1 - s with s = log2(e / 2^(10-CB) + 1),
-      // and the lanes read them there.
-      using Tw = typename A::Tw;
-      Tw* tl = reinterpret_cast<Tw*>(lds_raw + S::LDS);
-      const uint32_t nj = (1u << LOGN) | jbase;
-#pragma unroll
-      for (int r = 0; r < (S::TW1 + 63) / 64; ++r) {
-        const uint32_t e = l + 64u * r;
-        if (e < (uint32_t)S::TW1) {
-          const uint32_t s = 31u - (uint32_t)__builtin_clz((e >> (10 - CB)) + 1);
-          const uint32_t b = CB - 1 - s;
-          tl[e] = ld16(tw, (nj >> (b + 1)) + e - (((1u << s) - 1) << (10 - CB)));
-        }
-      }
+      // the first register pass's twiddles staged once per wavefront in LDS
+      const RowStage<LOGN, typename A::Tw> st(reinterpret_cast<typename A::Tw*>(lds_raw + S::LDS), jbase);
+      st.template fill<S::TW1, 64>(tw, l);
       slice_sync();
-      auto get = [&](int b, uint32_t base, uint32_t j) {
-        const int s = CB - 1 - b;
-        return tl[(((1u << s) - 1) << (10 - CB)) + (base | j) - (nj >> (b + 1))];
-      };
-      fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), get, ar);
+      fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), st, ar);
       wave_exchange(x, lds, p1, p2);
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
@@ -401,29 +420,14 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op.finish(r[k]));
-      // the second register pass's twiddles are shared by the lanes of a
-      // row: loaded once per wavefront into LDS (the forward pass's table
-      // layout, stages CB - 1 down to 4)
-      using Tw = typename A::Tw;
-      Tw* tl = reinterpret_cast<Tw*>(lds_raw + S::LDS);
-      const uint32_t nj = (1u << LOGN) | jbase;
-#pragma unroll
-      for (int rr = 0; rr < (S::TWI + 63) / 64; ++rr) {
-        const uint32_t e = l + 64u * rr;
-        if (e < (uint32_t)S::TWI) {
-          const uint32_t s = 31u - (uint32_t)__builtin_clz((e >> (10 - CB)) + 1);
-          const uint32_t b = CB - 1 - s;
-          tl[e] = ld16(tw, (nj >> (b + 1)) + e - (((1u << s) - 1) << (10 - CB)));
-        }
-      }
+      // the second register pass's twiddles (stages 4 .. CB - 1) staged once
+      // per wavefront in LDS; the exchanges' barriers order the staging
+      const RowStage<LOGN, typename A::Tw> st(reinterpret_cast<typename A::Tw*>(lds_raw + S::LDS), jbase);
+      st.template fill<S::TWI, 64>(tw, l);
       wave_exchange(x, lds, h, p2);
       inv_stages_get<LOGN, 0, 0, 3, A, true>(x, jbase + p2(0), row_get(lc.inv_row), ar, lc);
       wave_exchange(x, lds, p2, p1);
-      auto get = [&](int b, uint32_t base, uint32_t j) {
-        const int s = CB - 1 - b;
-        return tl[(((1u << s) - 1) << (10 - CB)) + (base | j) - (nj >> (b + 1))];
-      };
-      inv_stages_get<LOGN, CB - 4, 4, CB - 1, A, true>(x, jbase + p1(0), get, ar, lc);
+      inv_stages_get<LOGN, CB - 4, 4, CB - 1, A, true>(x, jbase + p1(0), st, ar, lc);
     } else {
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, jbase + g(k)));
@@ -863,8 +867,11 @@ __global__ __launch_bounds__(64) void rd_row_kernel(RescaleDecryptArgs a) {
       }
     }
     const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.inv));
+    const GPtr<typename A::Tw> tr = gld(reinterpret_cast<const typename A::Tw*>(lc.inv_row));
     wave_exchange(x, lds, g, p2);
-    inv_stages<LOGN, 0, 0, 3>(x, jbase + p2(0), tw, ar, lc);
+    inv_stages_get<LOGN, 0, 0, 3, A, true>(
+        x, jbase + p2(0), [&](int b, uint32_t, uint32_t s) { return ld16(tr, row_table_index(S::N, b, part, s, l)); },
+        ar, lc);
     wave_exchange(x, lds, p2, p1);
     inv_stages<LOGN, CB - 4, 4, CB - 1>(x, jbase + p1(0), tw, ar, lc);
     const GMut<uint64_t> out = gst(const_cast<uint64_t*>(jb.y));
