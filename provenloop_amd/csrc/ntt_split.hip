@@ -175,6 +175,43 @@ __device__ __forceinline__ void wave_exchange(V (&x)[16], V* lds, From from, To 
   slice_sync();
 }
 
+// The same exchange through half the LDS (1024 + 64 32-bit words): the
+// coefficients' low words first, then their high words. A register's low
+// word is free once written, so it takes its new value at once and no
+// register holds both layouts' words.
+template <class V, class From, class To>
+__device__ __forceinline__ void wave_exchange_half(V (&x)[16], uint32_t* lds, From from, To to) {
+  uint32_t lo[16], hi[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint64_t v = __builtin_bit_cast(uint64_t, x[k]);
+    lo[k] = (uint32_t)v;
+    hi[k] = (uint32_t)(v >> 32);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) lds[pad16(from(k))] = lo[k];
+  slice_sync();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) lo[k] = lds[pad16(to(k))];
+  slice_sync();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) lds[pad16(from(k))] = hi[k];
+  slice_sync();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) hi[k] = lds[pad16(to(k))];
+  slice_sync();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = __builtin_bit_cast(V, ((uint64_t)hi[k] << 32) | lo[k]);
+}
+
+template <bool HALF, class V, class From, class To>
+__device__ __forceinline__ void exchange_in(V (&x)[16], uint64_t* lds_raw, From from, To to) {
+  if constexpr (HALF)
+    wave_exchange_half(x, reinterpret_cast<uint32_t*>(lds_raw), from, to);
+  else
+    wave_exchange(x, reinterpret_cast<V*>(lds_raw), from, to);
+}
+
 // ------------------------------------------------------------------ column pass
 // Column geometry of wavefront `part`: CW adjacent columns, all 2^RB rows.
 template <int LOGN>
@@ -198,19 +235,19 @@ struct ColumnMap {
 };
 
 // Forward column pass on coefficients already in registers (Q1 layout, the
-// arithmetic's representation); writes the intermediate to dst (Q2).
-template <int LOGN, class A, bool BATCH = false>
+// arithmetic's representation); writes the intermediate to dst (Q2). HALF:
+// the exchange goes through half the LDS (wave_exchange_half).
+template <int LOGN, class A, bool BATCH = false, bool HALF = false>
 __device__ __forceinline__ void column_fwd_regs(typename A::V (&x)[16], uint64_t* dst, const LimbConst& lc,
                                                 const ColumnMap<LOGN>& m, const A& ar, uint64_t* lds_raw) {
   constexpr int CB = Split<LOGN>::CB;
   const GMut<uint64_t> gdst = gst(dst);
-  typename A::V* lds = reinterpret_cast<typename A::V*>(lds_raw);
   const GPtr<typename A::Tw> tw = gld(reinterpret_cast<const typename A::Tw*>(lc.fwd));
   // stages on bits >= LOGN - 4 (the Q1 registers): every lane's element
   // bits above the stage are zero, so the twiddle index is uniform (f = 0)
   fwd_stages_get<LOGN, LOGN - 4, LOGN - 1, LOGN - 4, A, BATCH>(
       x, 0u, [&](int, uint32_t base, uint32_t s) { return ld16_uniform(tw, base | s); }, ar);
-  wave_exchange(x, lds, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
+  exchange_in<HALF>(x, lds_raw, [&](uint32_t k) { return m.e1(k); }, [&](uint32_t k) { return m.e2(k); });
   fwd_stages<LOGN, CB, LOGN - 5, CB, A, BATCH>(x, m.j2(0), tw, ar);
 #pragma unroll
   for (int k = 0; k < 16; ++k) gdst[m.j2(k)] = ar.raw(x[k]);
@@ -254,7 +291,7 @@ __device__ __forceinline__ void column_pass(const uint64_t* __restrict__ src, ui
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = ar.load(op(src, m.j1(k)));
     }
-    column_fwd_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
+    column_fwd_regs<LOGN, A, false, true>(x, dst, lc, m, ar, lds_raw);
   } else {
     column_inv_regs<LOGN>(x, dst, lc, m, ar, lds_raw);
     const GMut<uint64_t> gdst = gst(dst);
@@ -461,15 +498,18 @@ __device__ __forceinline__ uint32_t column_part(uint32_t p) {
 // row pass the fused store operation; otherwise passes read and write the
 // destination only.
 template <int LOGN, bool INV, bool COLUMN, uint32_t LD, uint32_t ST>
-__global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
+__global__ __launch_bounds__(64)
+void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
   // the forward row pass with a fused rescale store, and the inverse row pass
   // with the product in its loads, also hold one register pass's twiddles
-  // (16-byte entries)
-  __shared__ uint64_t lds[S::LDS + (COLUMN                                   ? 0
-                                    : !INV && StoreOp<ST>::NAUX > 0          ? 2 * S::TW1
-                                    : INV && LD == NTT_LOAD_MULM             ? 2 * S::TWI
-                                                                             : 0)];
+  // (16-byte entries); the forward column passes exchange through half the
+  // LDS (their occupancy is then set by their registers: 20 or 24 wavefronts
+  // per CU instead of 18)
+  __shared__ uint64_t lds[!INV && COLUMN ? S::LDS / 2
+                          : S::LDS + (!INV && StoreOp<ST>::NAUX > 0 ? 2 * S::TW1
+                                      : INV && LD == NTT_LOAD_MULM  ? 2 * S::TWI
+                                                                    : 0)];
   const uint32_t job = blockIdx.x / S::PARTS;
   uint32_t part = blockIdx.x % S::PARTS;
   if constexpr (COLUMN) part = column_part<LOGN>(part);
