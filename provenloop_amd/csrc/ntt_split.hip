@@ -54,6 +54,7 @@ struct Split {
   // twiddle entries of a row-pass wavefront's first register pass (stages
   // CB-1 .. CB-4: 2^(9-b) entries of stage b over its 2^(10-CB) rows)
   static constexpr int TW1 = 15 << (10 - CB);
+  static constexpr int TW1S = 7 << (10 - CB);  // the same for stages CB-1 .. CB-3
   // and of an inverse row-pass wavefront's second register pass (stages 4 ..
   // CB-1)
   static constexpr int TWI = ((1 << (CB - 4)) - 1) << (10 - CB);
@@ -401,6 +402,15 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
       using U2 = uint64_t __attribute__((ext_vector_type(2)));
       typename SOp::Aux v[16];
       uint64_t c[16];
+      // the first register pass's twiddles of stages CB - 1 .. CB - 3 staged
+      // once per wavefront in LDS (those of stage CB - 4 are read from the
+      // table: staging them too would cost a workgroup per CU)
+      const RowStage<LOGN, typename A::Tw> st(reinterpret_cast<typename A::Tw*>(lds_raw + S::LDS), jbase);
+      st.template fill<S::TW1S, 64>(tw, l);
+      slice_sync();
+      fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(
+          x, jbase + p1(0),
+          [&](int b, uint32_t base, uint32_t j) { return b >= CB - 3 ? st(b, base, j) : ld16(tw, base | j); }, ar);
 #pragma unroll
       for (int k = 0; k < 16; k += 2) {
         const U2 a = ((GPtr<U2>)gld(so.aux))[(jbase + h(k)) >> 1];
@@ -412,11 +422,6 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
           v[k + 1].b = b.y;
         }
       }
-      // the first register pass's twiddles staged once per wavefront in LDS
-      const RowStage<LOGN, typename A::Tw> st(reinterpret_cast<typename A::Tw*>(lds_raw + S::LDS), jbase);
-      st.template fill<S::TW1, 64>(tw, l);
-      slice_sync();
-      fwd_stages_get<LOGN, CB - 4, CB - 1, CB - 4, A, true>(x, jbase + p1(0), st, ar);
       wave_exchange(x, lds, p1, p2);
 #pragma unroll
       for (int k = 0; k < 16; ++k) c[k] = so.prep(ar, v[k]);
@@ -507,7 +512,7 @@ void ntt_split_kernel(NttArgs a) {
   // LDS (their occupancy is then set by their registers: 20 or 24 wavefronts
   // per CU instead of 18)
   __shared__ uint64_t lds[!INV && COLUMN ? S::LDS / 2
-                          : S::LDS + (!INV && StoreOp<ST>::NAUX > 0 ? 2 * S::TW1
+                          : S::LDS + (!INV && StoreOp<ST>::NAUX > 0 ? 2 * S::TW1S
                                       : INV && LD == NTT_LOAD_MULM  ? 2 * S::TWI
                                                                     : 0)];
   const uint32_t job = blockIdx.x / S::PARTS;
