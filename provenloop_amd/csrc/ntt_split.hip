@@ -395,9 +395,10 @@ __device__ __forceinline__ void row_pass(const uint64_t* __restrict__ src, uint6
       // of the part, so they move as 16-byte accesses, half the memory
       // instructions of the lane-contiguous layout (this pass is bound by
       // the CUs' vector-memory address processing more than by its
-      // arithmetic). The operands are loaded behind the intermediate,
-      // before the butterflies, and combined after the first stages, so
-      // their latency overlaps the arithmetic.
+      // arithmetic). The operands are requested after the first register
+      // pass and combined after the exchange that follows it: held from the
+      // start, they cost the kernel a wavefront per SIMD (156 VGPRs against
+      // 127), which measured slower (106.3 against 104.1 us per token).
       auto h = [&](uint32_t k) { return (l << 1) + (k & 1) + ((k >> 1) << 7); };
       using U2 = uint64_t __attribute__((ext_vector_type(2)));
       typename SOp::Aux v[16];
