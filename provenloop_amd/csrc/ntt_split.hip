@@ -504,8 +504,7 @@ __device__ __forceinline__ uint32_t column_part(uint32_t p) {
 // row pass the fused store operation; otherwise passes read and write the
 // destination only.
 template <int LOGN, bool INV, bool COLUMN, uint32_t LD, uint32_t ST>
-__global__ __launch_bounds__(64)
-void ntt_split_kernel(NttArgs a) {
+__global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
   using S = Split<LOGN>;
   // the forward row pass with a fused rescale store, and the inverse row pass
   // with the product in its loads, also hold one register pass's twiddles
