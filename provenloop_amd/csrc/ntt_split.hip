@@ -556,11 +556,18 @@ __global__ __launch_bounds__(64) void ntt_split_kernel(NttArgs a) {
 // forward jobs i * nf .. i * nf + nf - 1, the order in which the rescale lists
 // them; each forward job's dst receives its column-pass intermediate, where
 // the forward row pass continues (with the rescale's store operation).
+// With fan (batches too small to fill the GPU), nf workgroups per inverse
+// job and part each repeat the inverse column pass and run one of the
+// forward passes (workgroup b: part b % PARTS of forward job b / PARTS), so
+// the launch takes one inverse and one forward pass instead of the inverse
+// and nf forward passes in turn.
 template <int LOGN>
-__global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs fwd, uint32_t nf) {
+__global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs fwd, uint32_t nf, uint32_t fan) {
   using S = Split<LOGN>;
   __shared__ uint64_t lds[S::LDS];
-  const uint32_t job = blockIdx.x / S::PARTS;
+  const uint32_t unit = blockIdx.x / S::PARTS;  // inverse job, or forward job with fan
+  const uint32_t job = fan ? unit / nf : unit;
+  const uint32_t f0 = fan ? unit % nf : 0, f1 = fan ? f0 + 1 : nf;
   const ColumnMap<LOGN> m(column_part<LOGN>(blockIdx.x % S::PARTS));
   const NttJob ij = inv.jobs[job];
   const LimbConst& lci = inv.lc[ij.limb];
@@ -579,7 +586,7 @@ __global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs
     for (int k = 0; k < 16; ++k) c[k] = ar.inv_store(x[k]);
   }
   // c mod q_l: FP64 on limbs below 2^41, else Barrett when c >= q_l
-  for (uint32_t f = 0; f < nf; ++f) {
+  for (uint32_t f = f0; f < f1; ++f) {
     const NttJob fj = fwd.jobs[(uint64_t)job * nf + f];
     const LimbConst& lcf = fwd.lc[fj.limb];
     const RescaleConst rc = fwd.rc[fj.limb];
@@ -603,6 +610,10 @@ __global__ __launch_bounds__(64) void rescale_column_kernel(NttArgs inv, NttArgs
   }
 }
 
+// Largest fanned-out rescale column launch: one round of that kernel's
+// wavefronts (3 per SIMD at its registers, 1024 SIMDs).
+constexpr uint32_t RESCALE_FAN_MAX_WAVES = 3072;
+
 template <int LOGN>
 static hipError_t launch_rescale_t(const NttArgs& inv, uint32_t ninv, const NttArgs& fwd, uint32_t nf, hipStream_t s) {
   using S = Split<LOGN>;
@@ -614,7 +625,11 @@ static hipError_t launch_rescale_t(const NttArgs& inv, uint32_t ninv, const NttA
     return hipGetLastError();
   });
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((rescale_column_kernel<LOGN>), dim3(ninv * S::PARTS), block, 0, s, inv, fwd, nf);
+  // a batch whose nf passes per inverse job would leave most SIMDs idle
+  // fans them out (RESCALE_FAN_MAX_WAVES)
+  const uint32_t fan = ninv * nf * S::PARTS <= RESCALE_FAN_MAX_WAVES ? 1u : 0u;
+  hipLaunchKernelGGL((rescale_column_kernel<LOGN>), dim3(ninv * S::PARTS * (fan ? nf : 1)), block, 0, s, inv, fwd, nf,
+                     fan);
   const hipError_t e2 = hipGetLastError();
   if (e2 != hipSuccess) return e2;
   return with_ops<false>(fwd.load, fwd.store, [&]<uint32_t LD, uint32_t ST>() -> hipError_t {
