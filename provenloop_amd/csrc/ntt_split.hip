@@ -51,10 +51,10 @@ struct Split {
   static constexpr int PARTS = N >> 10;          // wavefronts per limb-polynomial
   static constexpr int CW = 1 << (10 - RB);      // columns per column-pass wavefront
   static constexpr int LDS = 1024 + 64;          // one padding word per 16
-  // twiddle entries of a row-pass wavefront's first register pass (stages
-  // CB-1 .. CB-4: 2^(9-b) entries of stage b over its 2^(10-CB) rows)
-  static constexpr int TW1 = 15 << (10 - CB);
-  static constexpr int TW1S = 7 << (10 - CB);  // the same for stages CB-1 .. CB-3
+  // twiddle entries of stages CB-1 .. CB-3 of a forward row-pass wavefront's
+  // first register pass (2^(9-b) entries of stage b over its 2^(10-CB) rows;
+  // the staged ones, RowStage)
+  static constexpr int TW1S = 7 << (10 - CB);
   // and of an inverse row-pass wavefront's second register pass (stages 4 ..
   // CB-1)
   static constexpr int TWI = ((1 << (CB - 4)) - 1) << (10 - CB);
